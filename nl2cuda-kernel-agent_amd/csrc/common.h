@@ -1,0 +1,100 @@
+// Shared host/device helpers for the HIP kernels of every case library.
+//
+// Host side: a thread-local "last error" buffer, argument-check helpers that
+// run before any HIP call, and a launch check that turns a failed launch into
+// NL2K_ERR_HIP with the runtime's message.
+// Device side: 16-byte vector types, wave64 reductions and MFMA wrappers for
+// gfx950 (CDNA4).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstddef>
+#include <cstdint>
+#include <cstdio>
+
+#include "nl2k_status.h"
+
+namespace nl2k {
+
+// ---------------------------------------------------------------- host side
+struct ErrorSlot {
+  char text[512];
+};
+
+inline ErrorSlot& error_slot() {
+  static thread_local ErrorSlot slot = {{0}};
+  return slot;
+}
+
+inline int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(error_slot().text, sizeof(error_slot().text), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+inline int succeed() {
+  error_slot().text[0] = '\0';
+  return NL2K_SUCCESS;
+}
+
+inline bool aligned16(const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+// Checks the launch that was just enqueued.
+inline int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return fail(NL2K_ERR_HIP, "%s: kernel launch failed: %s", what,
+                hipGetErrorString(e));
+  return succeed();
+}
+
+inline int check_hip(hipError_t e, const char* what) {
+  if (e != hipSuccess)
+    return fail(NL2K_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return NL2K_SUCCESS;
+}
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// -------------------------------------------------------------- device side
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef double f64x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4 load4(const float* p) {
+  return *reinterpret_cast<const f32x4*>(p);
+}
+
+__device__ __forceinline__ void store4(float* p, f32x4 v) {
+  *reinterpret_cast<f32x4*>(p) = v;
+}
+
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+// One 16x16x4 fp32 MFMA: acc[m][n] += sum_k A[m][k] * B[k][n].
+// Lane l supplies A[l%16][l/16] in `a` and B[l/16][l%16] in `b`; the result
+// element [4*(l/16)+r][l%16] lives in register r of lane l.
+__device__ __forceinline__ f32x4 mfma16x4(float a, float b, f32x4 acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+}
+
+// Sum over all 64 lanes of a wave (result in every lane).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+}  // namespace nl2k

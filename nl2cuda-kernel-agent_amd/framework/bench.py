@@ -1,0 +1,199 @@
+"""Timing harness: candidate vs a baseline, forward and backward.
+
+Same protocol as the reference's framework/bench.py:27-178: warmup, then
+``iters`` timed calls with device events, geometric mean, ``repeats`` rounds
+to compute the coefficient of variation, up to ``max_retries`` re-measurements
+while CV > 5 %, backward timed with the autograd graph rebuilt outside the
+timed region.  Added for MI355X:
+
+  * a cache flush between timed iterations: a write of PROTOCOL.flush_bytes
+    (512 MiB) evicts the 4 MiB L2 of every XCD and the 256 MiB MALL, so each
+    timed call reads its operands from HBM (``flush=False`` disables it);
+  * ``time_ms`` is exposed for other drivers (the repository's bench.py).
+
+The baseline defaults to ``torch.compile(case.reference_forward)`` as in the
+reference; ``baseline="eager"`` times the eager reference instead.
+"""
+
+import math
+import os
+import statistics
+import sys
+
+sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+
+import torch  # noqa: E402
+
+from framework.protocol import PROTOCOL, dtype_of  # noqa: E402
+
+_FLUSH = {}
+
+
+def _flush_buffer(device):
+    key = str(device)
+    if key not in _FLUSH:
+        _FLUSH[key] = torch.empty(PROTOCOL.flush_bytes // 4, dtype=torch.float32,
+                                  device=device)
+    return _FLUSH[key]
+
+
+def flush_caches(device="cuda"):
+    """Overwrite a 512 MiB buffer so no operand stays in L2 or the MALL."""
+    _flush_buffer(device).fill_(0.0)
+
+
+def _geomean(xs):
+    return math.exp(sum(math.log(max(x, 1e-12)) for x in xs) / len(xs))
+
+
+def time_ms(fn, warmup=None, iters=None, flush=True, setup=None, device="cuda"):
+    """Per-iteration device time (ms) of ``fn`` between two HIP events.
+
+    ``setup`` (optional) runs before each iteration outside the timed region
+    and returns the callable to time (used for backward: it rebuilds the
+    graph).  Returns the list of times.
+    """
+    p = PROTOCOL
+    warmup = p.warmup if warmup is None else warmup
+    iters = p.iters if iters is None else iters
+    for _ in range(warmup):
+        (setup() if setup else fn)()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(iters):
+        call = setup() if setup else fn
+        if flush:
+            flush_caches(device)
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        call()
+        end.record()
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(end))
+    return times
+
+
+def _summarize(kind, geomeans, cv_threshold):
+    mean = statistics.mean(geomeans)
+    cv = (statistics.pstdev(geomeans) / mean) if mean > 0 else float("inf")
+    return {"kind": kind, "geomeans_ms": geomeans, "geomean_ms": _geomean(geomeans),
+            "cv": cv, "ok": cv <= cv_threshold}
+
+
+def _collect_with_retry(kind, one_round):
+    p = PROTOCOL
+    best = None
+    for attempt in range(p.max_retries + 1):
+        s = _summarize(kind, one_round(), p.cv_threshold)
+        s["attempts"] = attempt + 1
+        if best is None or s["cv"] < best["cv"]:
+            best = s
+        if s["ok"]:
+            break
+    return best
+
+
+def forward_geomean_cv(fn, inputs, params, flush=True):
+    p = PROTOCOL
+    detached = {k: v.detach() for k, v in inputs.items()}
+
+    def step():
+        with torch.no_grad():
+            fn(detached, params)
+
+    def one_round():
+        return [_geomean(time_ms(step, p.warmup, p.iters, flush)) for _ in range(p.repeats)]
+
+    return _collect_with_retry("forward", one_round)
+
+
+def backward_geomean_cv(fn, inputs, params, grad_inputs, G, flush=True):
+    p = PROTOCOL
+
+    def build_graph():
+        loc = {}
+        for k, v in inputs.items():
+            t = v.detach().clone()
+            if k in grad_inputs:
+                t.requires_grad_(True)
+            loc[k] = t
+        out = fn(loc, params)
+
+        def do_bwd():
+            out.backward(G)
+        return do_bwd
+
+    def one_round():
+        return [_geomean(time_ms(None, p.warmup, p.iters, flush, setup=build_graph))
+                for _ in range(p.repeats)]
+
+    return _collect_with_retry("backward", one_round)
+
+
+def compare(case, candidate, device=None, seed=0, baseline="compile", flush=True):
+    """Time candidate vs baseline; returns (report_str, passed) like the reference."""
+    p = PROTOCOL
+    if device is None:
+        device = "cuda" if torch.cuda.is_available() else "cpu"
+    assert str(device).startswith("cuda"), "timing needs the GPU"
+    dtype = dtype_of(case.dtype)
+
+    inputs = {k: v.to(device) for k, v in
+              case.make_inputs(seed, dtype, "cpu", requires_grad=False).items()}
+    with torch.no_grad():
+        out = candidate(inputs, case.params)
+    g = torch.Generator(device="cpu").manual_seed(777)
+    G = torch.randn(out.shape, dtype=out.dtype, generator=g).to(device)
+
+    base_fn = torch.compile(case.reference_forward) if baseline == "compile" \
+        else case.reference_forward
+    base_name = "baseline(torch.compile)" if baseline == "compile" else "baseline(eager)"
+
+    lines = [f"=== timing: case={case.name} (HIP events, geomean, flush={flush}) ===",
+             f"grad_inputs={case.grad_inputs} params={case.params} dtype={case.dtype}"]
+    results = {}
+    with_bwd = len(case.grad_inputs) > 0
+    for name, fn in [(base_name, base_fn), ("candidate", candidate)]:
+        fres = forward_geomean_cv(fn, inputs, case.params, flush)
+        bres = backward_geomean_cv(fn, inputs, case.params, case.grad_inputs, G, flush) \
+            if with_bwd else None
+        results[name] = (fres, bres)
+        lines.append(f"\n[{name}]")
+        lines.append(f"  forward : {fres['geomean_ms']:.4f} ms  CV={fres['cv']*100:.2f}%  "
+                     f"x{fres['attempts']}  {'ok' if fres['ok'] else 'CV over threshold'}")
+        if bres:
+            lines.append(f"  backward: {bres['geomean_ms']:.4f} ms  CV={bres['cv']*100:.2f}%  "
+                         f"x{bres['attempts']}  {'ok' if bres['ok'] else 'CV over threshold'}")
+
+    bf, bb = results[base_name]
+    cf, cb = results["candidate"]
+    fwd_speedup = bf["geomean_ms"] / cf["geomean_ms"]
+    lines.append("\n[speedup candidate vs baseline]")
+    lines.append(f"  forward : {fwd_speedup:.4f}x  (target >={p.speedup_target}x) "
+                 f"{'PASS' if fwd_speedup >= p.speedup_target else 'FAIL'}")
+    passed = fwd_speedup >= p.speedup_target
+    cvs = [bf, cf]
+    if with_bwd:
+        bwd_speedup = bb["geomean_ms"] / cb["geomean_ms"]
+        lines.append(f"  backward: {bwd_speedup:.4f}x  (target >={p.speedup_target}x) "
+                     f"{'PASS' if bwd_speedup >= p.speedup_target else 'FAIL'}")
+        passed = passed and bwd_speedup >= p.speedup_target
+        cvs += [bb, cb]
+    cv_ok = all(r["ok"] for r in cvs)
+    passed = passed and cv_ok
+    if not cv_ok:
+        lines.append("  CV > 5% present: result invalid, re-measure")
+    lines.append(f"\n=== verdict: {'PASS' if passed else 'FAIL'} ===")
+    return "\n".join(lines), passed
+
+
+def parse_verdict(report, passed):
+    """One-line machine-readable summary, same grammar as the reference's
+    bench_case.py:_parse_verdict (skill/scripts/bench_case.py:33-54):
+    ``VERDICT=<PASS|BENCH_FAIL|CV_INVALID> fwd=<x>x bwd=<x>x cv_ok=<0|1>``."""
+    import re
+    sp = dict(re.findall(r"(forward|backward)\s*:\s*([0-9.]+)x\s*\(target", report))
+    cv_ok = 0 if "CV > 5% present" in report else 1
+    verdict = "CV_INVALID" if cv_ok == 0 else ("PASS" if passed else "BENCH_FAIL")
+    return f"VERDICT={verdict} fwd={sp.get('forward', '?')}x bwd={sp.get('backward', '?')}x cv_ok={cv_ok}"

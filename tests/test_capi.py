@@ -1,0 +1,98 @@
+"""C-ABI checks that need no GPU: every library loads, exports every symbol
+its header in include/ declares, and rejects bad arguments with the right
+NL2K_* status before touching the device."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from framework import loader
+
+import __graft_entry__ as entry
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INCLUDE = os.path.join(REPO, "include")
+
+# header -> op module that loads the library implementing it
+HEADERS = {"rbf.h": "cases.rbf.op"}
+
+STATUS = {}
+with open(os.path.join(INCLUDE, "nl2k_status.h")) as _f:
+    for _name, _val in re.findall(r"#define\s+(NL2K_\w+)\s+\(?(-?\d+)\)?", _f.read()):
+        STATUS[_name] = int(_val)
+
+
+def declared_functions(header):
+    with open(os.path.join(INCLUDE, header)) as f:
+        text = f.read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    text = re.sub(r"#[^\n]*", "", text)
+    return sorted(set(re.findall(r"\b([A-Za-z_]\w*)\s*\([^;{)]*(?:\([^)]*\)[^;{)]*)*\)\s*;", text)))
+
+
+def _load(modname):
+    import importlib
+    mod = importlib.import_module(modname)
+    lib = loader.load_library(mod.LIB_NAME, mod.SOURCES, mod.KERNEL_DIR)
+    return mod.bind_library(lib)
+
+
+def test_every_op_module_has_a_header():
+    assert sorted(HEADERS.values()) == sorted(entry.OP_MODULES)
+
+
+@pytest.mark.parametrize("header", sorted(HEADERS))
+def test_library_exports_every_declared_symbol(header):
+    names = declared_functions(header)
+    assert names, f"no declarations parsed from {header}"
+    lib = _load(HEADERS[header])
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, f"{header}: not exported: {missing}"
+
+
+def test_rbf_argument_validation_without_gpu():
+    lib = _load("cases.rbf.op")
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: every call below fails validation
+    null = None
+    st = lib.rbf_forward_f32(fake, fake, fake, -1, 4, 64, 0.5, null)
+    assert st == STATUS["NL2K_ERR_SHAPE"] and b"N >= 0" in lib.rbf_last_error()
+    st = lib.rbf_forward_f32(fake, fake, fake, 4, 4, 0, 0.5, null)
+    assert st == STATUS["NL2K_ERR_SHAPE"]
+    st = lib.rbf_forward_f32(null, fake, fake, 4, 4, 64, 0.5, null)
+    assert st == STATUS["NL2K_ERR_NULL"]
+    st = lib.rbf_forward_f32(fake, fake, fake, 1 << 40, 4, 64, 0.5, null)
+    assert st == STATUS["NL2K_ERR_OVERFLOW"]
+    # empty problem: nothing to do, success without any launch
+    assert lib.rbf_forward_f32(null, null, null, 0, 5, 64, 0.5, null) == 0
+    assert lib.rbf_last_error() == b""
+    # backward: workspace too small is reported before any launch
+    need = lib.rbf_backward_workspace_bytes(4096, 4096, 64)
+    assert need == (16 * 4096 + 16 * 4096) * 64 * 4
+    st = lib.rbf_backward_f32(fake, fake, fake, fake, fake, fake, 4096, 4096, 64, 0.5,
+                              null, 0, null)
+    assert st == STATUS["NL2K_ERR_WORKSPACE"] and b"workspace" in lib.rbf_last_error()
+    st = lib.rbf_backward_f32(null, fake, fake, fake, fake, fake, 8, 8, 64, 0.5, null, 0, null)
+    assert st == STATUS["NL2K_ERR_NULL"]
+
+
+def test_rbf_workspace_plan():
+    lib = _load("cases.rbf.op")
+    # 2048: 128-edge regions -> 16 x 16; 8192: 512-edge regions -> 16 x 16
+    assert lib.rbf_backward_workspace_bytes(2048, 2048, 64) == 2 * 16 * 2048 * 64 * 4
+    assert lib.rbf_backward_workspace_bytes(8192, 8192, 64) == 2 * 16 * 8192 * 64 * 4
+    # a single region needs no workspace; other D use the generic path
+    assert lib.rbf_backward_workspace_bytes(64, 64, 64) == 0
+    assert lib.rbf_backward_workspace_bytes(4096, 4096, 32) == 0
+
+
+def test_loader_refuses_without_gpu():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("GPU present")
+    from cases.rbf import op
+    op._lib.cache_clear()
+    with pytest.raises(RuntimeError, match="needs an MI355X"):
+        op._lib()
