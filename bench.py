@@ -7,7 +7,7 @@ seed 0 and copied to HBM before timing.  One step = one forward
 librbf_hip.so, on preallocated device buffers.
 
 Timing: W untimed warmup steps, then exactly K steps between two device
-synchronisations.  Before every step a 512 MiB buffer is overwritten so the
+synchronisations.  Before every step a 512 MiB buffer is read so the
 step reads its operands from HBM, not from L2 or the 256 MiB MALL; HIP events
 on the launch stream bracket the forward and the backward calls of each step
 (the flush is outside them).  ``ms_per_step`` is the mean of the bracketed
@@ -196,7 +196,7 @@ def main():
         "dtype": "f32",
         "data": "synthetic (host-seeded N(0,1)/8 inputs, N(0,1) dK; copied to HBM before timing)",
         "config": {"workload": f"rbf fwd+bwd N=M={n} D={d} gamma={gamma}", "N": n, "M": m, "D": d,
-                   "gamma": gamma, "flush_between_steps": "512 MiB write (L2 + MALL)"},
+                   "gamma": gamma, "flush_between_steps": "512 MiB read (evicts L2 + MALL without dirty lines)"},
         "fwd_us": round(fwd_avg * 1e3, 2),
         "bwd_us": round(bwd_avg * 1e3, 2),
         "fwd_gbs": round(fb / (fwd_avg * 1e-3) / 1e9, 1),

@@ -6,9 +6,13 @@ to compute the coefficient of variation, up to ``max_retries`` re-measurements
 while CV > 5 %, backward timed with the autograd graph rebuilt outside the
 timed region.  Added for MI355X:
 
-  * a cache flush between timed iterations: a write of PROTOCOL.flush_bytes
+  * a cache flush between timed iterations: a read of PROTOCOL.flush_bytes
     (512 MiB) evicts the 4 MiB L2 of every XCD and the 256 MiB MALL, so each
-    timed call reads its operands from HBM (``flush=False`` disables it);
+    timed call reads its operands from HBM (``flush=False`` disables it).  The
+    flush reads rather than writes: a 512 MiB write leaves ~256 MB of dirty
+    MALL lines whose write-back then competes with the timed kernel's reads
+    (measured on MI355X: a linear 256 MiB read runs at ~3.0 TB/s right after
+    a write flush and at ~6.0 TB/s after a read flush);
   * ``time_ms`` is exposed for other drivers (the repository's bench.py).
 
 The baseline defaults to ``torch.compile(case.reference_forward)`` as in the
@@ -32,14 +36,17 @@ _FLUSH = {}
 def _flush_buffer(device):
     key = str(device)
     if key not in _FLUSH:
-        _FLUSH[key] = torch.empty(PROTOCOL.flush_bytes // 4, dtype=torch.float32,
-                                  device=device)
+        buf = torch.zeros(PROTOCOL.flush_bytes // 4, dtype=torch.float32, device=device)
+        torch.cuda.synchronize()
+        _FLUSH[key] = (buf, torch.empty(1, dtype=torch.float32, device=device))
     return _FLUSH[key]
 
 
 def flush_caches(device="cuda"):
-    """Overwrite a 512 MiB buffer so no operand stays in L2 or the MALL."""
-    _flush_buffer(device).fill_(0.0)
+    """Read a 512 MiB buffer so no operand stays in L2 or the MALL (and no
+    dirty lines are left behind to be written back during the next call)."""
+    buf, sink = _flush_buffer(device)
+    torch.sum(buf, dim=0, out=sink[0])
 
 
 def _geomean(xs):

@@ -70,7 +70,7 @@ def test_rbf_argument_validation_without_gpu():
     assert lib.rbf_last_error() == b""
     # backward: workspace too small is reported before any launch
     need = lib.rbf_backward_workspace_bytes(4096, 4096, 64)
-    assert need == (16 * 4096 + 16 * 4096) * 64 * 4
+    assert need == (16 * 4096 + 16 * 4096) * 65 * 4
     st = lib.rbf_backward_f32(fake, fake, fake, fake, fake, fake, 4096, 4096, 64, 0.5,
                               null, 0, null)
     assert st == STATUS["NL2K_ERR_WORKSPACE"] and b"workspace" in lib.rbf_last_error()
@@ -80,11 +80,13 @@ def test_rbf_argument_validation_without_gpu():
 
 def test_rbf_workspace_plan():
     lib = _load("cases.rbf.op")
-    # 2048: 128-edge regions -> 16 x 16; 8192: 512-edge regions -> 16 x 16
-    assert lib.rbf_backward_workspace_bytes(2048, 2048, 64) == 2 * 16 * 2048 * 64 * 4
-    assert lib.rbf_backward_workspace_bytes(8192, 8192, 64) == 2 * 16 * 8192 * 64 * 4
-    # a single region needs no workspace; other D use the generic path
-    assert lib.rbf_backward_workspace_bytes(64, 64, 64) == 0
+    # Per region slot: a [rows, 64] partial contraction plus a [rows] partial
+    # row/column sum of W.  2048: 128-edge regions -> 16 x 16 slots;
+    # 8192: 256-edge regions -> 32 x 32; 64 x 64: a single region.
+    assert lib.rbf_backward_workspace_bytes(2048, 2048, 64) == 2 * 16 * 2048 * 65 * 4
+    assert lib.rbf_backward_workspace_bytes(8192, 8192, 64) == 2 * 32 * 8192 * 65 * 4
+    assert lib.rbf_backward_workspace_bytes(64, 64, 64) == 2 * 64 * 65 * 4
+    # other feature widths use the generic path, which needs no workspace
     assert lib.rbf_backward_workspace_bytes(4096, 4096, 32) == 0
 
 
