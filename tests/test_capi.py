@@ -16,7 +16,7 @@ REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 INCLUDE = os.path.join(REPO, "include")
 
 # header -> op module that loads the library implementing it
-HEADERS = {"rbf.h": "cases.rbf.op"}
+HEADERS = {"rbf.h": "cases.rbf.op", "layernorm.h": "cases.layernorm.op"}
 
 STATUS = {}
 with open(os.path.join(INCLUDE, "nl2k_status.h")) as _f:
