@@ -89,6 +89,19 @@ def cpu_baseline(size, d, gamma, budget_s):
     }
 
 
+def copy_calibration():
+    """A plain copy kernel of known size: reads and writes 256 MiB per launch."""
+    import torch
+    n = (256 << 20) // 4
+    src = torch.ones(n, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"copy calibration: 10 x {n * 4} bytes", flush=True)
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -97,7 +110,13 @@ def main():
     ap.add_argument("--size", type=int, default=4096)
     ap.add_argument("--cpu-budget", type=float, default=15.0,
                     help="seconds of CPU work for the cpu_baseline sample (0 = skip)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 256 MiB device-to-device copy 10 times (the known-size "
+                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args()
+
+    if args.copy_calibration:
+        return copy_calibration()
 
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
@@ -206,7 +225,7 @@ def main():
         "bwd_tflops": round(bwd_tf, 2),
         "pct_fp32_roofline": round(100 * (ff + bf) / (step_ms * 1e-3) / 1e12 / FP32_PEAK_TFLOPS, 2),
         "roofline": {
-            "kernel": "rbf_backward_f32 (rbf_bwd_d64_kernel + rbf_sum_slots_kernel x2)",
+            "kernel": "rbf_backward_f32 (rbf_bwd_d64_kernel + rbf_bwd_reduce_kernel)",
             "bound": "mfma",
             "achieved": round(bwd_tf, 3),
             "peak": FP32_PEAK_TFLOPS,

@@ -8,23 +8,31 @@
 //   dY[j] = -2 gamma * sum_i W[i,j] (Y[j] - X[i])
 //
 // Design (D == 64 fast path):
-//  * Forward: K[i,j] = exp(-gamma * max(|x_i|^2 + |y_j|^2 - 2 x_i.y_j, 0)).
-//    The cross term runs on fp32 MFMA (v_mfma_f32_16x16x4_f32).  Each wave
-//    owns a 64x64 tile of K and loads its 64 X rows and 64 Y rows straight
-//    into MFMA operand registers (X and Y are L2 resident).  The contraction
-//    index k is permuted consistently for both operands so that every lane
-//    loads 16 contiguous bytes per load; the row norms fall out of the same
-//    registers.  The exp epilogue runs from the accumulators and each lane
-//    writes 4 consecutive K entries of one row with a 16-byte store.
-//  * Backward: one pass over dK and K.  A workgroup (8 waves) owns a region of
-//    RI x RJ entries of W and walks it in 64x64 tiles that are staged through
-//    LDS (double buffered: W = dK o K, and the matching 64-row slices of X and
-//    Y).  Waves 0-3 run the contraction W . Y (dX side), waves 4-7 run
-//    W^T . X (dY side), both on fp32 MFMA.  The dX accumulators live for one
-//    64-row chunk, the dY accumulators for the whole region, so each region
-//    emits one partial dX slice (over its RJ columns) and one partial dY slice
-//    (over its RI rows); a small kernel sums the slices.  The row and column
-//    sums of W are taken from the same MFMA operand registers.
+//  * Forward: K[i,j] = exp2(min(2 kappa x_i.y_j - kappa (|x_i|^2 + |y_j|^2), 0))
+//    with kappa = gamma log2(e).  The cross term runs on fp32 MFMA
+//    (v_mfma_f32_16x16x4_f32).  Work unit = 256 rows x 64 columns of K; a
+//    workgroup of four waves walks a contiguous range of units.  Each wave
+//    keeps its 64 X rows in MFMA operand registers (with their norms) for as
+//    long as the row block lasts, and the unit's 64 Y rows are staged once
+//    per workgroup in LDS (double buffered, norms alongside) while the
+//    previous unit runs on the matrix cores.  The contraction index is
+//    permuted identically for both operands so every lane moves 16
+//    contiguous bytes per load.  The exp epilogue runs from the accumulators
+//    and each lane writes 4 consecutive K entries of a row (16-byte stores).
+//  * Backward: one pass over dK and K.  A workgroup (8 waves) owns a region
+//    of R x R entries of W = dK o K (R = 256 at N = M = 4096, one region per
+//    CU) and walks it in 64x64 tiles.  Waves 4-7 only stage: they load dK and
+//    K three tiles ahead into registers, form W into the LDS tile buffer of
+//    the next tile, and stage the next 64-row X chunk (transposed).  Waves
+//    0-3 only compute: per tile both contractions W . Y (rows, accumulated
+//    over the region's columns and flushed per 64-row chunk) and W^T . X
+//    (columns, accumulated over the whole region) on fp32 MFMA, with the row
+//    and column sums of W taken from the same operand registers.  Each region
+//    writes raw partial contractions and partial sums to its workspace slot;
+//    rbf_bwd_reduce_kernel sums the slots and applies
+//    dX = -2 gamma (rowsum(W) X - W Y), dY = -2 gamma (colsum(W) Y - W^T X).
+//  * Other feature widths and misaligned pointers use the generic kernels
+//    (direct sums over d, one thread per output entry / row).
 #include <algorithm>
 #include <cmath>
 #include <cstdint>

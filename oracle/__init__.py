@@ -13,10 +13,11 @@ Modules (each function cites the reference file:line it restates):
   layernorm.py  float64 forward/backward and the torch CPU path
   scan.py       exact int64 / float64 prefix sums and the torch CPU path
   spmv.py       float64 CSR products, the Zipf row-length recipe, torch CPU path
-  native.py     ctypes binding of csrc/oracle.c (C restatement, built into
-                oracle/lib/liboracle.so by oracle/Makefile)
-  refbuild.py   builds oracle/_ref/ from the reference's own C++ sources
-                (cases/rbf/delivery/rbf_test.cu) when /root/reference exists
+  native.py     ctypes bindings of csrc/oracle.c (C restatement, built into
+                oracle/lib/liboracle.so by oracle/Makefile) and of
+                oracle/_ref/librbf_ref.so, which `make -C oracle ref` builds
+                from the reference's own cases/rbf/delivery/rbf_test.cu
+                (through ref/rbf_ref_cpu.cpp) when /root/reference exists
 
 How each function is pinned is listed in the module docstrings; functions
 without an independent pin say "parity unpinned".
