@@ -16,7 +16,8 @@ REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 INCLUDE = os.path.join(REPO, "include")
 
 # header -> op module that loads the library implementing it
-HEADERS = {"rbf.h": "cases.rbf.op", "layernorm.h": "cases.layernorm.op"}
+HEADERS = {"rbf.h": "cases.rbf.op", "layernorm.h": "cases.layernorm.op",
+           "scan.h": "cases.scan.op"}
 
 STATUS = {}
 with open(os.path.join(INCLUDE, "nl2k_status.h")) as _f:
@@ -98,3 +99,25 @@ def test_loader_refuses_without_gpu():
     op._lib.cache_clear()
     with pytest.raises(RuntimeError, match="needs an MI355X"):
         op._lib()
+
+
+def test_scan_argument_validation_and_plan_without_gpu():
+    lib = _load("cases.scan.op")
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: every call below fails validation
+    st = lib.scan_forward_f32(fake, fake, -1, 16, None, 0, None)
+    assert st == STATUS["NL2K_ERR_SHAPE"] and b"rows" in lib.scan_last_error()
+    st = lib.scan_backward_f32(fake, fake, 4, 0, None, 0, None)
+    assert st == STATUS["NL2K_ERR_SHAPE"]
+    st = lib.scan_forward_i32_i64(fake, fake, 2, 2**31, None, 0, None)
+    assert st == STATUS["NL2K_ERR_OVERFLOW"]
+    st = lib.scan_forward_f32(None, fake, 4, 16, None, 0, None)
+    assert st == STATUS["NL2K_ERR_NULL"]
+    # rows of one 4096-element chunk need no workspace; longer rows need one
+    # 8-byte slot per chunk plus one word
+    assert lib.scan_workspace_bytes(4096, 4096) == 0
+    assert lib.scan_workspace_bytes(64, 65536) == (64 * 16 + 1) * 8
+    assert lib.scan_workspace_bytes(2, 2**21 + 5) == (2 * 171 + 1) * 8  # 513 tiles -> 171 chunks of 3
+    need = lib.scan_workspace_bytes(64, 65536)
+    st = lib.scan_forward_f32(fake, fake, 64, 65536, fake, need - 8, None)
+    assert st == STATUS["NL2K_ERR_WORKSPACE"]
+    assert lib.scan_forward_f32(fake, fake, 0, 65536, None, 0, None) == 0  # nothing to do
