@@ -1,0 +1,62 @@
+/*
+ * libspmv_hip.so -- CSR sparse x dense products (SpMV at D = 1, SpMM at D > 1),
+ * fp32 values, int32 or int64 indices, MI355X.
+ *
+ *   A: [M, K] in CSR (row_ptr[M + 1], col_idx[nnz], vals[nnz]); X: [K, D];
+ *   forward   Y[m, :]  = sum_{p in row m} vals[p] * X[col_idx[p], :]
+ *   backward  dvals[p] = dY[row(p), :] . X[col_idx[p], :]
+ *             dX       = A^T dY  (dX[col_idx[p], :] += vals[p] * dY[row(p), :])
+ *
+ * Dense arrays are row-major fp32 device arrays owned by the caller; kernels
+ * run on `stream`; nothing is allocated and no state is kept.  Preconditions
+ * on the structure (row_ptr[0] = 0, non-decreasing, row_ptr[M] = nnz,
+ * 0 <= col_idx < K) cannot be checked without reading device memory; the
+ * kernels clamp every index they load into range, so a malformed structure
+ * gives wrong numbers, never an out-of-bounds access.  The forward is
+ * deterministic; dX is accumulated with fp32 atomics (order varies between
+ * runs, as in the reference).
+ *
+ * Reference interface replaced: the pybind entries `spmv_forward(row_ptr,
+ * col_idx, vals, X) -> Y` and `spmv_backward(row_ptr, col_idx, vals, X,
+ * grad_Y) -> [grad_vals, grad_X]` of cases/spmv/kernels/spmv.cu:199-288,
+ * called from cases/spmv/op.py:24-57 (there: int64 indices only).
+ */
+#ifndef NL2K_SPMV_H
+#define NL2K_SPMV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#include "nl2k_status.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Y [M, D] = A X (spmv.cu:199-239, `spmv_forward`). */
+int spmv_forward_f32_i32(const int32_t* row_ptr, const int32_t* col_idx, const float* vals,
+                         const float* X, float* Y, int64_t M, int64_t K, int64_t D,
+                         int64_t nnz, hipStream_t stream);
+int spmv_forward_f32_i64(const int64_t* row_ptr, const int64_t* col_idx, const float* vals,
+                         const float* X, float* Y, int64_t M, int64_t K, int64_t D,
+                         int64_t nnz, hipStream_t stream);
+
+/* dvals [nnz] and dX [K, D] from dY [M, D] (spmv.cu:241-288,
+ * `spmv_backward`).  Either output may be NULL to skip it; dX is fully
+ * written (zeroed, then accumulated). */
+int spmv_backward_f32_i32(const int32_t* row_ptr, const int32_t* col_idx, const float* vals,
+                          const float* X, const float* dY, float* dvals, float* dX,
+                          int64_t M, int64_t K, int64_t D, int64_t nnz, hipStream_t stream);
+int spmv_backward_f32_i64(const int64_t* row_ptr, const int64_t* col_idx, const float* vals,
+                          const float* X, const float* dY, float* dvals, float* dX,
+                          int64_t M, int64_t K, int64_t D, int64_t nnz, hipStream_t stream);
+
+const char* spmv_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NL2K_SPMV_H */

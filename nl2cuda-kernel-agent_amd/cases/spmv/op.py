@@ -1,0 +1,120 @@
+"""CSR SpMM / SpMV candidate: autograd wrapper over libspmv_hip.so.
+
+Mirrors the reference's cases/spmv/op.py:24-57: ``_CSRSpMMFunction`` saves
+(row_ptr, col_idx, vals, X) and returns (None, None, grad_vals, grad_X);
+``candidate`` / ``forward_only`` keep the dict interface.  The argument
+checks follow spmv.cu:167-197 (GPU tensors, fp32 values, 1-D structure of
+matching lengths, rank-2 X with positive sizes), with int32 indices accepted
+beside int64 (row_ptr and col_idx must share the type).  There is no CPU
+path: without a GPU the library refuses to load.
+"""
+
+import functools
+import os
+
+import torch
+
+from framework import capi
+from framework.loader import load_kernel
+
+KERNEL_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "kernels")
+LIB_NAME = "spmv_hip"
+SOURCES = ["spmv.hip"]
+
+
+def bind_library(lib):
+    V, I64 = capi.c_void_p, capi.c_int64
+    for t in ("i32", "i64"):
+        capi.bind(lib, f"spmv_forward_f32_{t}", [V, V, V, V, V, I64, I64, I64, I64, V])
+        capi.bind(lib, f"spmv_backward_f32_{t}", [V, V, V, V, V, V, V, I64, I64, I64, I64, V])
+    capi.bind_last_error(lib, "spmv_last_error")
+    return lib
+
+
+@functools.lru_cache(maxsize=1)
+def _lib():
+    return bind_library(load_kernel(LIB_NAME, SOURCES, base_dir=KERNEL_DIR))
+
+
+def _suffix(row_ptr, col_idx):
+    capi.require(row_ptr.dtype == col_idx.dtype, "row_ptr and col_idx must share a dtype")
+    capi.require(row_ptr.dtype in (torch.int32, torch.int64), "row_ptr must be int64 or int32")
+    return "i32" if row_ptr.dtype == torch.int32 else "i64"
+
+
+def _validate(row_ptr, col_idx, vals, X):
+    for name, t in (("row_ptr", row_ptr), ("col_idx", col_idx), ("vals", vals), ("X", X)):
+        capi.require(t.is_cuda, f"{name} must be a GPU tensor")
+    capi.require(vals.dtype == torch.float32, "vals must be float32")
+    capi.require(X.dtype == torch.float32, "X must be float32")
+    capi.require(X.dim() == 2, "X must be a rank-2 tensor")
+    capi.require(X.size(0) > 0 and X.size(1) > 0, "X dimensions must be positive")
+    capi.require(row_ptr.dim() == 1 and row_ptr.numel() >= 1, "row_ptr must have shape [M + 1]")
+    capi.require(col_idx.dim() == 1, "col_idx must have shape [nnz]")
+    capi.require(vals.dim() == 1, "vals must have shape [nnz]")
+    capi.require(col_idx.numel() == vals.numel(), "col_idx and vals must have the same length")
+    return _suffix(row_ptr, col_idx)
+
+
+def spmv_forward(row_ptr, col_idx, vals, X):
+    t = _validate(row_ptr, col_idx, vals, X)
+    lib = _lib()
+    row_ptr, col_idx, vals, X = (a.contiguous() for a in (row_ptr, col_idx, vals, X))
+    M = row_ptr.numel() - 1
+    K, D = X.shape
+    Y = torch.empty((M, D), dtype=torch.float32, device=X.device)
+    with torch.cuda.device(X.device):
+        st = getattr(lib, f"spmv_forward_f32_{t}")(
+            capi.ptr(row_ptr), capi.ptr(col_idx), capi.ptr(vals), capi.ptr(X), capi.ptr(Y),
+            M, K, D, vals.numel(), capi.stream_of(X))
+    capi.check(st, lib.spmv_last_error, "spmv_forward")
+    return Y
+
+
+def spmv_backward(row_ptr, col_idx, vals, X, grad_Y, need_vals=True, need_X=True):
+    t = _validate(row_ptr, col_idx, vals, X)
+    capi.require(grad_Y.is_cuda and grad_Y.dtype == torch.float32, "grad_Y must be a float32 GPU tensor")
+    M = row_ptr.numel() - 1
+    capi.require(grad_Y.dim() == 2 and grad_Y.size(0) == M and grad_Y.size(1) == X.size(1),
+                 "grad_Y must have shape [M, D]")
+    lib = _lib()
+    row_ptr, col_idx, vals, X, grad_Y = (a.contiguous() for a in (row_ptr, col_idx, vals, X, grad_Y))
+    K, D = X.shape
+    grad_vals = torch.empty_like(vals) if need_vals else None
+    grad_X = torch.empty_like(X) if need_X else None
+    with torch.cuda.device(X.device):
+        st = getattr(lib, f"spmv_backward_f32_{t}")(
+            capi.ptr(row_ptr), capi.ptr(col_idx), capi.ptr(vals), capi.ptr(X), capi.ptr(grad_Y),
+            capi.ptr(grad_vals) if need_vals else None, capi.ptr(grad_X) if need_X else None,
+            M, K, D, vals.numel(), capi.stream_of(X))
+    capi.check(st, lib.spmv_last_error, "spmv_backward")
+    return grad_vals, grad_X
+
+
+class _CSRSpMMFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, row_ptr, col_idx, vals, X):
+        row_ptr = row_ptr.contiguous()
+        col_idx = col_idx.contiguous()
+        vals = vals.contiguous()
+        X = X.contiguous()
+        ctx.save_for_backward(row_ptr, col_idx, vals, X)
+        return spmv_forward(row_ptr, col_idx, vals, X)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        row_ptr, col_idx, vals, X = ctx.saved_tensors
+        grad_vals, grad_X = spmv_backward(row_ptr, col_idx, vals, X, grad_output.contiguous(),
+                                          need_vals=ctx.needs_input_grad[2],
+                                          need_X=ctx.needs_input_grad[3])
+        return None, None, grad_vals, grad_X
+
+
+def candidate(inputs, params):
+    del params
+    return _CSRSpMMFunction.apply(inputs["row_ptr"], inputs["col_idx"], inputs["vals"], inputs["X"])
+
+
+def forward_only(inputs, params):
+    del params
+    return spmv_forward(inputs["row_ptr"], inputs["col_idx"], inputs["vals"], inputs["X"])

@@ -17,7 +17,7 @@ INCLUDE = os.path.join(REPO, "include")
 
 # header -> op module that loads the library implementing it
 HEADERS = {"rbf.h": "cases.rbf.op", "layernorm.h": "cases.layernorm.op",
-           "scan.h": "cases.scan.op"}
+           "scan.h": "cases.scan.op", "spmv.h": "cases.spmv.op"}
 
 STATUS = {}
 with open(os.path.join(INCLUDE, "nl2k_status.h")) as _f:
@@ -121,3 +121,19 @@ def test_scan_argument_validation_and_plan_without_gpu():
     st = lib.scan_forward_f32(fake, fake, 64, 65536, fake, need - 8, None)
     assert st == STATUS["NL2K_ERR_WORKSPACE"]
     assert lib.scan_forward_f32(fake, fake, 0, 65536, None, 0, None) == 0  # nothing to do
+
+
+def test_spmv_argument_validation_without_gpu():
+    lib = _load("cases.spmv.op")
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: every call below fails validation
+    st = lib.spmv_forward_f32_i32(fake, fake, fake, fake, fake, -1, 4, 1, 0, None)
+    assert st == STATUS["NL2K_ERR_SHAPE"] and b"M >= 0" in lib.spmv_last_error()
+    st = lib.spmv_forward_f32_i64(fake, fake, fake, fake, fake, 4, 0, 1, 0, None)
+    assert st == STATUS["NL2K_ERR_SHAPE"]
+    st = lib.spmv_forward_f32_i32(fake, fake, fake, fake, fake, 4, 4, 1, 2**31, None)
+    assert st == STATUS["NL2K_ERR_OVERFLOW"]
+    st = lib.spmv_forward_f32_i64(None, fake, fake, fake, fake, 4, 4, 1, 8, None)
+    assert st == STATUS["NL2K_ERR_NULL"]
+    st = lib.spmv_backward_f32_i32(fake, None, fake, fake, fake, fake, fake, 4, 4, 1, 8, None)
+    assert st == STATUS["NL2K_ERR_NULL"]
+    assert lib.spmv_forward_f32_i32(fake, fake, fake, fake, fake, 0, 4, 1, 0, None) == 0

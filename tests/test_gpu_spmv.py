@@ -1,0 +1,190 @@
+"""CSR SpMV / SpMM parity on the GPU (libspmv_hip.so) against the float64
+oracle at atol = rtol = 1e-3: the acceptance workload (2^20 x 2^20 power-law,
+int32 and int64 indices, D = 1, forward and backward), the reference's
+default case through verify_all, structures with empty rows, runs of empty
+rows longer than the staged window, long rows, K = 1, nnz = 0, feature
+widths across every SpMM lane class, misaligned value arrays, determinism
+and the adjoint identities."""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from framework.verify import verify_all
+from oracle import spmv as osp
+
+pytestmark = pytest.mark.gpu
+
+
+def _close(name, got, ref, atol=1e-3, rtol=1e-3):
+    got = got.detach().cpu().double().numpy()
+    ref = np.asarray(ref, dtype=np.float64)
+    assert got.shape == ref.shape, (name, got.shape, ref.shape)
+    err = np.abs(got - ref)
+    max_abs = float(err.max()) if err.size else 0.0
+    print(f"  {name}: max_abs={max_abs:.3e}")
+    assert np.all(err <= atol + rtol * np.abs(ref)), f"{name}: max_abs {max_abs:.3e}"
+
+
+def _csr(lens, k, d, seed, index_dtype=torch.int64):
+    rng = np.random.default_rng(seed)
+    lens = np.asarray(lens, dtype=np.int64)
+    ptr = np.zeros(lens.size + 1, np.int64)
+    np.cumsum(lens, out=ptr[1:])
+    col = rng.integers(0, k, int(ptr[-1]))
+    g = torch.Generator().manual_seed(seed)
+    vals = torch.randn(int(ptr[-1]), generator=g)
+    X = torch.randn(k, d, generator=g)
+    return (torch.from_numpy(ptr).to(index_dtype), torch.from_numpy(col).to(index_dtype), vals, X)
+
+
+def _check(ptr, col, vals, X, seed=0, check_bwd=True):
+    from cases.spmv import op
+    M = ptr.numel() - 1
+    dY = torch.randn(M, X.shape[1], generator=torch.Generator().manual_seed(seed + 10_000))
+    y = op.spmv_forward(ptr.cuda(), col.cuda(), vals.cuda(), X.cuda())
+    torch.cuda.synchronize()
+    _close("y", y, osp.forward_f64(ptr.numpy(), col.numpy(), vals.numpy(), X.numpy()))
+    if check_bwd:
+        dv, dX = op.spmv_backward(ptr.cuda(), col.cuda(), vals.cuda(), X.cuda(), dY.cuda())
+        torch.cuda.synchronize()
+        rdv, rdX = osp.backward_f64(ptr.numpy(), col.numpy(), vals.numpy(), X.numpy(), dY.numpy())
+        _close("dvals", dv, rdv)
+        _close("dX", dX, rdX)
+    return y
+
+
+@pytest.fixture(scope="module")
+def zipf_inputs():
+    from cases.spmv import reference as ref
+    return ref.make_zipf_inputs(1 << 20, 1 << 20, 1, 0, torch.int32)
+
+
+def test_spmv_zipf_baseline_int32(zipf_inputs):
+    announce("spmv zipf 2^20 int32 D=1 fwd+bwd")
+    t = zipf_inputs
+    y = _check(t["row_ptr"], t["col_idx"], t["vals"], t["X"])
+    from cases.spmv import op
+    y2 = op.spmv_forward(t["row_ptr"].cuda(), t["col_idx"].cuda(), t["vals"].cuda(), t["X"].cuda())
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2), "forward is not deterministic"
+
+
+def test_spmv_zipf_int64_matches_int32(zipf_inputs):
+    announce("spmv zipf 2^20 int64 == int32")
+    from cases.spmv import op
+    t = zipf_inputs
+    args32 = [t["row_ptr"].cuda(), t["col_idx"].cuda(), t["vals"].cuda(), t["X"].cuda()]
+    args64 = [t["row_ptr"].long().cuda(), t["col_idx"].long().cuda()] + args32[2:]
+    y32 = op.spmv_forward(*args32)
+    y64 = op.spmv_forward(*args64)
+    dY = torch.randn(y32.shape, generator=torch.Generator().manual_seed(3)).cuda()
+    dv32, _ = op.spmv_backward(*args32, dY, need_X=False)
+    dv64, dX64 = op.spmv_backward(*args64, dY)
+    torch.cuda.synchronize()
+    assert torch.equal(y32, y64)
+    assert torch.equal(dv32, dv64)
+    # adjoint identities at full size: <A x, dy> = <x, A^T dy> = sum vals * dvals
+    lhs = float((y64.double() * dY.double()).sum())
+    assert np.isclose(lhs, float((args32[3].double() * dX64.double()).sum()), rtol=1e-4)
+    assert np.isclose(lhs, float((args32[2].double() * dv64.double()).sum()), rtol=1e-4)
+
+
+def test_spmv_verify_all_reference_defaults():
+    announce("spmv verify_all (reference defaults M=K=4096 D=64 int64)")
+    from cases.spmv import CASE, op
+    ok, report = verify_all(CASE, op.candidate, device="cuda")
+    print(report)
+    assert ok, report
+
+
+def _lens(kind, m, k, rng):
+    if kind == "small":
+        return rng.integers(0, 10, m)
+    if kind == "mostly_empty":
+        return np.where(rng.random(m) < 0.9, 0, rng.integers(0, min(k, 2000) + 1, m))
+    if kind == "ones":
+        return np.ones(m, np.int64)
+    if kind == "one_long":
+        lens = np.zeros(m, np.int64)
+        lens[m // 3] = k
+        return lens
+    if kind == "ends_only":  # runs of empty rows far longer than the staged window
+        lens = np.zeros(m, np.int64)
+        lens[1] = 5
+        lens[m - 2] = 300
+        return lens
+    if kind == "zipf":
+        return np.minimum(rng.zipf(1.5, m), k)
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("kind,m,k,d", [
+    ("small", 1000, 500, 1), ("mostly_empty", 3000, 3000, 1), ("ones", 257, 100, 1),
+    ("one_long", 2000, 60000, 1), ("ends_only", 5000, 400, 1), ("zipf", 20000, 5000, 1),
+    ("small", 4000, 1, 1), ("small", 1, 10, 1), ("small", 500, 300, 3), ("small", 500, 300, 4),
+    ("zipf", 300, 200, 17), ("zipf", 300, 200, 64), ("small", 100, 100, 100),
+    ("small", 100, 50, 256), ("one_long", 64, 64, 300), ("ends_only", 700, 90, 8)])
+def test_spmv_structures(kind, m, k, d):
+    announce(f"spmv {kind} M={m} K={k} D={d}")
+    rng = np.random.default_rng(m + k + d)
+    lens = _lens(kind, m, k, rng)
+    for idx in (torch.int64, torch.int32):
+        _check(*_csr(lens, k, d, m + d, idx))
+
+
+def test_spmv_no_nonzeros():
+    announce("spmv nnz = 0")
+    from cases.spmv import op
+    ptr = torch.zeros(101, dtype=torch.int64)
+    col = torch.zeros(0, dtype=torch.int64)
+    vals = torch.zeros(0)
+    X = torch.randn(7, 1)
+    y = op.spmv_forward(ptr.cuda(), col.cuda(), vals.cuda(), X.cuda())
+    dv, dX = op.spmv_backward(ptr.cuda(), col.cuda(), vals.cuda(), X.cuda(), torch.ones(100, 1).cuda())
+    torch.cuda.synchronize()
+    assert torch.all(y == 0) and y.shape == (100, 1)
+    assert dv.numel() == 0 and torch.all(dX == 0)
+
+
+def test_spmv_misaligned_values():
+    announce("spmv misaligned vals / X (scalar paths)")
+    from cases.spmv import op
+    ptr, col, vals, X = _csr(np.random.default_rng(1).integers(0, 20, 900), 700, 1, 9)
+    buf = torch.empty(vals.numel() + 1, device="cuda")
+    buf[1:].copy_(vals.cuda())
+    y = op.spmv_forward(ptr.cuda(), col.cuda(), buf[1:], X.cuda())
+    torch.cuda.synchronize()
+    _close("y (misaligned vals)", y, osp.forward_f64(ptr.numpy(), col.numpy(), vals.numpy(), X.numpy()))
+    ptr, col, vals, X = _csr(np.random.default_rng(2).integers(0, 20, 300), 200, 64, 10)
+    xb = torch.empty(X.numel() + 1, device="cuda")
+    xb[1:].copy_(X.reshape(-1).cuda())
+    y = op.spmv_forward(ptr.cuda(), col.cuda(), vals.cuda(), xb[1:].view(200, 64))
+    torch.cuda.synchronize()
+    _close("y (misaligned X)", y, osp.forward_f64(ptr.numpy(), col.numpy(), vals.numpy(), X.numpy()))
+
+
+def test_spmv_autograd_partial_grads():
+    announce("spmv autograd, X only")
+    from cases.spmv import op
+    ptr, col, vals, X = _csr(np.random.default_rng(4).integers(1, 30, 400), 300, 16, 11)
+    Xd = X.cuda().requires_grad_(True)
+    y = op.candidate({"row_ptr": ptr.cuda(), "col_idx": col.cuda(), "vals": vals.cuda(), "X": Xd}, {})
+    dY = torch.randn(y.shape, generator=torch.Generator().manual_seed(5))
+    y.backward(dY.cuda())
+    torch.cuda.synchronize()
+    _, rdX = osp.backward_f64(ptr.numpy(), col.numpy(), vals.numpy(), X.numpy(), dY.numpy())
+    _close("dX", Xd.grad, rdX)
+
+
+def test_spmv_rejects_bad_arguments():
+    announce("spmv argument checks")
+    from cases.spmv import op
+    ptr, col, vals, X = _csr([1, 2], 4, 1, 0)
+    with pytest.raises(RuntimeError, match="share a dtype"):
+        op.spmv_forward(ptr.cuda(), col.int().cuda(), vals.cuda(), X.cuda())
+    with pytest.raises(RuntimeError, match="same length"):
+        op.spmv_forward(ptr.cuda(), col.cuda(), vals[:1].cuda(), X.cuda())
+    with pytest.raises(RuntimeError, match="rank-2"):
+        op.spmv_forward(ptr.cuda(), col.cuda(), vals.cuda(), X.reshape(-1).cuda())
