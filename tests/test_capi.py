@@ -137,3 +137,21 @@ def test_spmv_argument_validation_without_gpu():
     st = lib.spmv_backward_f32_i32(fake, None, fake, fake, fake, fake, fake, 4, 4, 1, 8, None)
     assert st == STATUS["NL2K_ERR_NULL"]
     assert lib.spmv_forward_f32_i32(fake, fake, fake, fake, fake, 0, 4, 1, 0, None) == 0
+
+
+DELIVERY = os.path.join(REPO, "nl2cuda-kernel-agent_amd", "cases", "rbf", "delivery")
+
+
+def test_delivery_archive_exports_every_declared_symbol():
+    """librbf.a (built by __graft_entry__.build) defines every function of
+    include/rbf_delivery.h and of include/rbf.h."""
+    import subprocess
+    archive = os.path.join(DELIVERY, "librbf.a")
+    if not os.path.exists(archive):
+        pytest.skip("delivery not built")
+    out = subprocess.run(["nm", "--defined-only", archive], capture_output=True, text=True,
+                         check=True).stdout
+    defined = set(re.findall(r" T (\w+)", out))
+    for header in ("rbf_delivery.h", "rbf.h"):
+        missing = [n for n in declared_functions(header) if n not in defined]
+        assert not missing, f"{header}: not in librbf.a: {missing}"
