@@ -194,7 +194,7 @@ __global__ __launch_bounds__(256, 2) void rbf_fwd_d64_kernel(
         }
         float* dst = K + (size_t)i * M + j;
         if (full) {
-          __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(dst));
+          store4(dst, o);
         } else if (i < N && j < M) {
           if (vec_store && j + 3 < M) {
             store4(dst, o);
@@ -266,106 +266,134 @@ __global__ __launch_bounds__(512) void rbf_bwd_d64_kernel(
   const int n_jc = (cols + kTile - 1) / kTile;
   const int n_tiles = n_ic * n_jc;
 
-  // Region prologue (all waves): Yt <- Y[jbase .. jbase+RJ), transposed, with
-  // lanes along j so the transposed LDS writes hit consecutive banks.
-  for (int f = tid; f < RJ * 16; f += 512) {
+  // Staging-wave state (declared for all waves; only waves 4-7 use it).
+  const int ptid = tid - 256;
+  // W: float4 (row (p>>4) + 16 s, cols 4 (p & 15)..), s = 0..3.
+  const int srow = (ptid >> 4) & 15;
+  const int scol = (ptid & 15) * 4;
+  // X chunk: row p & 63 (lanes along rows), float4 columns (p>>6) + 4 s.
+  const int xrow = ptid & 63;
+  const int xcol = ((ptid >> 6) & 3) * 4;
+  f32x4 g_dk[3][4], g_k[3][4], g_x[3][4];
+  bool g_ok[3][4];
+  auto load_stage = [&](int t, f32x4 (&dk)[4], f32x4 (&kk)[4], bool (&ok)[4]) {
+    const int ic = t / n_jc, jc = t - ic * n_jc;
+    const int ib = ibase + ic * kTile;
+    const int jb = jbase + jc * kTile;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int gi = ib + srow + 16 * s;
+      const int gj = jb + scol;
+      const int ci = min(gi, N - 1);
+      if (kVecNM) {
+        ok[s] = gi < N && gj < M;
+        const size_t o = (size_t)ci * M + min(gj, M - 4);
+        dk[s] = load4(dK + o);
+        kk[s] = load4(Kf + o);
+      } else {
+        ok[s] = gi < N;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const size_t o = (size_t)ci * M + min(gj + u, M - 1);
+          const bool in = gj + u < M;
+          const float a = dK[o], b = Kf[o];
+          dk[s][u] = in ? a : 0.f;
+          kk[s][u] = in ? b : 0.f;
+        }
+      }
+    }
+  };
+  auto commit_stage = [&](int t, const f32x4 (&dk)[4], const f32x4 (&kk)[4],
+                          const bool (&ok)[4]) {
+    float* dst = P[t & 1];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      store4(&dst[(srow + 16 * s) * kLds + scol], ok[s] ? dk[s] * kk[s] : zero4());
+  };
+  auto load_x = [&](int ic, f32x4 (&xs)[4]) {
+    const size_t r = (size_t)min(ibase + ic * kTile + xrow, N - 1);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) xs[s] = load4(X + r * kD + xcol + 16 * s);
+  };
+  auto commit_x = [&](int ic, const f32x4 (&xs)[4]) {
+    float* dst = Xt[ic & 1];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) dst[(xcol + 16 * s + u) * kLds + xrow] = xs[s][u];
+  };
+  // X chunk published at step t: the one after the chunk of tile t (clamped;
+  // at the last chunk that rewrites the chunk in use with identical bits).
+  auto x_chunk = [&](int t) { return min(t / n_jc + 1, n_ic - 1); };
+
+  // Tile 0's loads go out first, then every wave stages the region's Y rows
+  // (Yt <- Y[jbase .. jbase+RJ), transposed, lanes along j so the transposed
+  // LDS writes hit consecutive banks) while they are in flight.
+  if (wave >= 4) {
+    load_stage(0, g_dk[0], g_k[0], g_ok[0]);
+    load_x(0, g_x[0]);
+  }
+  constexpr int kYtPerThread = RJ * 16 / 512;
+  f32x4 yv[kYtPerThread];
+#pragma unroll
+  for (int k = 0; k < kYtPerThread; ++k) {
+    const int f = tid + 512 * k;
+    yv[k] = load4(Y + (size_t)min(jbase + f % RJ, M - 1) * kD + (f / RJ) * 4);
+  }
+#pragma unroll
+  for (int k = 0; k < kYtPerThread; ++k) {
+    const int f = tid + 512 * k;
     const int j = f % RJ;
     const int c = (f / RJ) * 4;
-    const f32x4 v = load4(Y + (size_t)min(jbase + j, M - 1) * kD + c);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) Yt[(c + u) * kYtLds + j] = v[u];
+    for (int u = 0; u < 4; ++u) Yt[(c + u) * kYtLds + j] = yv[k][u];
   }
+  // Both roles pass 1 + n_steps barriers; the staging loop is unrolled by
+  // three, so the compute side pads its tile barriers up to n_steps.
+  const int n_steps = (n_tiles + 2) / 3 * 3;
 
   if (wave >= 4) {
     // ------------------------------------------------------ staging waves
-    const int ptid = tid - 256;
-    // W: float4 (row (p>>4) + 16 s, cols 4 (p & 15)..), s = 0..3.
-    const int srow = ptid >> 4;
-    const int scol = (ptid & 15) * 4;
-    // X chunk: row p & 63 (lanes along rows), float4 columns (p>>6) + 4 s.
-    const int xrow = ptid & 63;
-    const int xcol = (ptid >> 6) * 4;
-    f32x4 g_dk[3][4], g_k[3][4], g_x[4];
-    bool g_ok[3][4];
-    auto load_stage = [&](int t, f32x4 (&dk)[4], f32x4 (&kk)[4], bool (&ok)[4]) {
-      const int ic = t / n_jc, jc = t - ic * n_jc;
-      const int ib = ibase + ic * kTile;
-      const int jb = jbase + jc * kTile;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int gi = ib + srow + 16 * s;
-        const int gj = jb + scol;
-        const int ci = min(gi, N - 1);
-        if (kVecNM) {
-          ok[s] = gi < N && gj < M;
-          const size_t o = (size_t)ci * M + min(gj, M - 4);
-          dk[s] = load4(dK + o);
-          kk[s] = load4(Kf + o);
-        } else {
-          ok[s] = gi < N;
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const size_t o = (size_t)ci * M + min(gj + u, M - 1);
-            const bool in = gj + u < M;
-            const float a = dK[o], b = Kf[o];
-            dk[s][u] = in ? a : 0.f;
-            kk[s][u] = in ? b : 0.f;
-          }
-        }
-      }
-    };
-    auto commit_stage = [&](int t, const f32x4 (&dk)[4], const f32x4 (&kk)[4],
-                            const bool (&ok)[4]) {
-      float* dst = P[t & 1];
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        store4(&dst[(srow + 16 * s) * kLds + scol], ok[s] ? dk[s] * kk[s] : zero4());
-    };
-    auto load_x = [&](int ic) {
-      const size_t r = (size_t)min(ibase + ic * kTile + xrow, N - 1);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) g_x[s] = load4(X + r * kD + xcol + 16 * s);
-    };
-    auto commit_x = [&](int ic) {
-      float* dst = Xt[ic & 1];
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int u = 0; u < 4; ++u) dst[(xcol + 16 * s + u) * kLds + xrow] = g_x[s][u];
-    };
-    // One staging step per tile t (all before the tile's barrier): issue the
-    // next chunk's X loads at the chunk's first tile and publish them at its
-    // last, publish W of tile t+1 (loaded two steps ago), issue the loads of
-    // tile t+3.  Three register stages keep two tiles of loads in flight
-    // while a third is published.  The stages are addressed statically (the
-    // loop below is unrolled by three): a runtime stage index would be
-    // if-converted into selects on the loaded data, forcing a wait right
-    // after each load.
-    auto step = [&](int t, f32x4 (&ldk)[4], f32x4 (&lk)[4], bool (&lok)[4],
-                    const f32x4 (&cdk)[4], const f32x4 (&ck)[4], const bool (&cok)[4]) {
-      const int ic = t / n_jc, jc = t - ic * n_jc;
-      const bool more = ic + 1 < n_ic;
-      if (jc == 0 && more) load_x(ic + 1);
-      if (n_jc > 1 && jc == n_jc - 1 && more) commit_x(ic + 1);
-      if (t + 1 < n_tiles) commit_stage(t + 1, cdk, ck, cok);
-      if (t + 3 < n_tiles) load_stage(t + 3, ldk, lk, lok);
-      if (n_jc == 1 && more) commit_x(ic + 1);
-      __syncthreads();
-    };
-
-    load_x(0);
-    load_stage(0, g_dk[0], g_k[0], g_ok[0]);
-    if (n_tiles > 1) load_stage(1, g_dk[1], g_k[1], g_ok[1]);
-    if (n_tiles > 2) load_stage(2, g_dk[2], g_k[2], g_ok[2]);
-    commit_x(0);
+    // Every step t runs the same straight-line sequence (no branches, so the
+    // loads of later tiles stay in flight across steps): load tile t+3 and
+    // the X chunk step t+2 publishes into the register stage published last
+    // step, then publish stage (t+1) % 3, loaded two steps ago: W of tile
+    // t+1 and the X chunk after tile t's.  Every wait is therefore on loads
+    // two steps old (the memory counter retires in order, so one younger
+    // consumer would make every step wait for the previous step's loads).
+    // Indices are clamped: loads past the last tile fetch valid data nobody
+    // uses; commits past it fill the idle P buffer.  A republished X chunk rewrites the buffer the compute waves
+    // are reading only with identical bits.  The three register stages are
+    // addressed statically (the loop is unrolled by three): a runtime stage
+    // index would be if-converted into selects on the loaded data, forcing a
+    // wait right after each load.
+    load_stage(min(1, n_tiles - 1), g_dk[1], g_k[1], g_ok[1]);
+    load_x(x_chunk(0), g_x[1]);
+    load_stage(min(2, n_tiles - 1), g_dk[2], g_k[2], g_ok[2]);
+    load_x(x_chunk(1), g_x[2]);
+    commit_x(0, g_x[0]);
     commit_stage(0, g_dk[0], g_k[0], g_ok[0]);
     __syncthreads();
+    auto step = [&](int t, f32x4 (&ldk)[4], f32x4 (&lk)[4], bool (&lok)[4], f32x4 (&lx)[4],
+                    const f32x4 (&cdk)[4], const f32x4 (&ck)[4], const bool (&cok)[4],
+                    const f32x4 (&cx)[4]) {
+      // The scheduling fences keep each step's work between its barriers:
+      // hoisting the next step's W products above the barrier would make
+      // them wait on loads issued only one step earlier.
+      __builtin_amdgcn_sched_barrier(0);
+      load_stage(min(t + 3, n_tiles - 1), ldk, lk, lok);
+      load_x(x_chunk(t + 2), lx);
+      commit_x(x_chunk(t), cx);
+      commit_stage(t + 1, cdk, ck, cok);
+      __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();
+    };
     // Tile t's data sits in stage t % 3: step t publishes stage (t+1) % 3 and
     // refills stage t % 3 (free since step t-1 published it) with tile t+3.
-    for (int t = 0; t < n_tiles; t += 3) {
-      step(t, g_dk[0], g_k[0], g_ok[0], g_dk[1], g_k[1], g_ok[1]);
-      if (t + 1 < n_tiles) step(t + 1, g_dk[1], g_k[1], g_ok[1], g_dk[2], g_k[2], g_ok[2]);
-      if (t + 2 < n_tiles) step(t + 2, g_dk[2], g_k[2], g_ok[2], g_dk[0], g_k[0], g_ok[0]);
+    for (int t = 0; t < n_steps; t += 3) {
+      step(t, g_dk[0], g_k[0], g_ok[0], g_x[0], g_dk[1], g_k[1], g_ok[1], g_x[1]);
+      step(t + 1, g_dk[1], g_k[1], g_ok[1], g_x[1], g_dk[2], g_k[2], g_ok[2], g_x[2]);
+      step(t + 2, g_dk[2], g_k[2], g_ok[2], g_x[2], g_dk[0], g_k[0], g_ok[0], g_x[0]);
     }
     return;
   }
@@ -449,6 +477,8 @@ __global__ __launch_bounds__(512) void rbf_bwd_d64_kernel(
       }
     }
   }
+
+  for (int t = n_tiles; t < n_steps; ++t) __syncthreads();
 
   const size_t slot = (size_t)ri * M;
 #pragma unroll
