@@ -1,0 +1,180 @@
+"""Roofline report for the follow-on cases (layernorm, scan, spmv) on one GPU.
+
+For each case's acceptance workload this times every C-ABI entry point
+directly on preallocated device buffers: a 512 MiB read flush before each
+call (so operands come from HBM, not L2 or the MALL), HIP events on the
+launch stream around the call, ``--iters`` timed calls after ``--warmup``.
+Achieved GB/s = algorithmic bytes / mean time (each input read once, each
+output written once; the byte counts are stated per entry), against the
+MI355X HBM peak of 8 TB/s.  Event times include the launch (about 6 us for
+an empty kernel on this box); rocprofv3 kernel times
+(framework/profile.py stats) give the kernel-only figure.
+
+Usage:  python nl2cuda-kernel-agent_amd/framework/roofline.py [--case all|layernorm|scan|spmv]
+Prints one JSON line per measurement and a closing table.
+"""
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+
+PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, PKG)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def _timer(dev, iters, warmup):
+    import torch
+    from framework.bench import flush_caches
+
+    def time_us(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        stream = torch.cuda.current_stream(dev)
+        for _ in range(iters):
+            flush_caches(dev)
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e3)
+        ts.sort()
+        trim = ts[len(ts) // 10: len(ts) - len(ts) // 10] or ts
+        return sum(trim) / len(trim)
+
+    return time_us
+
+
+def _check(st, lib, err):
+    if st != 0:
+        raise RuntimeError(getattr(lib, err)().decode())
+
+
+def layernorm(dev, time_us):
+    import torch
+    from framework import capi
+    from cases.layernorm import op
+    lib = op._lib()
+    B, D = 8192, 4096
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(B, D, generator=g).to(dev)
+    w = (1 + 0.1 * torch.randn(D, generator=g)).to(dev)
+    b = (0.1 * torch.randn(D, generator=g)).to(dev)
+    dy = torch.randn(B, D, generator=g).to(dev)
+    y, dx = torch.empty_like(x), torch.empty_like(x)
+    mean, rstd = torch.empty(B, device=dev), torch.empty(B, device=dev)
+    dw, db = torch.empty(D, device=dev), torch.empty(D, device=dev)
+    wsb = lib.layernorm_backward_workspace_bytes(B, D)
+    ws = torch.empty(max(wsb // 4, 1), device=dev)
+    s, P = capi.stream_of(x), capi.ptr
+    out = []
+    t = time_us(lambda: _check(lib.layernorm_forward_f32(P(x), P(w), P(b), P(y), P(mean), P(rstd),
+                                                         B, D, 1e-5, s), lib, "layernorm_last_error"))
+    out.append(("layernorm", "forward_f32 [8192,4096]", t, 8 * B * D + 8 * D + 8 * B,
+                "read x, w, bias; write y, mean, rstd"))
+    t = time_us(lambda: _check(lib.layernorm_backward_f32(P(dy), P(x), P(w), P(mean), P(rstd), P(dx),
+                                                          P(dw), P(db), B, D, P(ws), wsb, s),
+                               lib, "layernorm_last_error"))
+    out.append(("layernorm", "backward_f32 [8192,4096]", t, 12 * B * D + 12 * D + 8 * B,
+                "read dy, x, w, mean, rstd; write dx, dw, dbias"))
+    return out
+
+
+def scan(dev, time_us):
+    import torch
+    from framework import capi
+    from cases.scan import op
+    lib = op._lib()
+    out = []
+    for R, D in ((64, 65536), (4096, 4096)):
+        g = torch.Generator().manual_seed(0)
+        x = (torch.rand(R, D, generator=g) * 2 - 1).to(dev)
+        xi = torch.randint(-1000, 1001, (R, D), generator=g, dtype=torch.int32).to(dev)
+        y = torch.empty_like(x)
+        y64 = torch.empty(R, D, dtype=torch.int64, device=dev)
+        y32 = torch.empty_like(xi)
+        wsb = lib.scan_workspace_bytes(R, D)
+        ws = torch.empty(max(wsb // 8, 1), dtype=torch.int64, device=dev)
+        s, P = capi.stream_of(x), capi.ptr
+        shape = f"[{R},{D}]"
+        for name, fn, nbytes, what in (
+                ("forward_f32", lambda: lib.scan_forward_f32(P(x), P(y), R, D, P(ws), wsb, s),
+                 8 * R * D, "read x, write y (f32)"),
+                ("backward_f32", lambda: lib.scan_backward_f32(P(x), P(y), R, D, P(ws), wsb, s),
+                 8 * R * D, "read dy, write dx (f32)"),
+                ("forward_i32_i64", lambda: lib.scan_forward_i32_i64(P(xi), P(y64), R, D, P(ws), wsb, s),
+                 12 * R * D, "read int32, write int64"),
+                ("forward_i32", lambda: lib.scan_forward_i32(P(xi), P(y32), R, D, P(ws), wsb, s),
+                 8 * R * D, "read int32, write int32")):
+            t = time_us(lambda fn=fn: _check(fn(), lib, "scan_last_error"))
+            out.append(("scan", f"{name} {shape}", t, nbytes, what))
+    return out
+
+
+def spmv(dev, time_us):
+    import torch
+    from framework import capi
+    from cases.spmv import op, reference as ref
+    lib = op._lib()
+    M = K = 1 << 20
+    t = ref.make_zipf_inputs(M, K, 1, 0, torch.int32)
+    ptr, col, vals, X = (t[k].to(dev) for k in ("row_ptr", "col_idx", "vals", "X"))
+    nnz = vals.numel()
+    Y = torch.empty(M, 1, device=dev)
+    dY = torch.randn(M, 1, generator=torch.Generator().manual_seed(1)).to(dev)
+    dv, dX = torch.empty_like(vals), torch.empty_like(X)
+    s, P = capi.stream_of(X), capi.ptr
+    base = 4 * (M + 1) + 8 * nnz
+    out = []
+    tt = time_us(lambda: _check(lib.spmv_forward_f32_i32(P(ptr), P(col), P(vals), P(X), P(Y), M, K, 1,
+                                                        nnz, s), lib, "spmv_last_error"))
+    out.append(("spmv", "forward_f32_i32 zipf 2^20 D=1", tt, base + 4 * K + 4 * M,
+                "read row_ptr, col_idx, vals, x; write y"))
+    tt = time_us(lambda: _check(lib.spmv_backward_f32_i32(P(ptr), P(col), P(vals), P(X), P(dY), None,
+                                                         P(dX), M, K, 1, nnz, s), lib, "spmv_last_error"))
+    out.append(("spmv", "backward dx only, zipf 2^20", tt, base + 4 * M + 4 * K,
+                "read structure, dy; write dx"))
+    tt = time_us(lambda: _check(lib.spmv_backward_f32_i32(P(ptr), P(col), P(vals), P(X), P(dY), P(dv),
+                                                         P(dX), M, K, 1, nnz, s), lib, "spmv_last_error"))
+    out.append(("spmv", "backward dvals + dx, zipf 2^20", tt, base + 4 * M + 8 * K + 4 * nnz,
+                "read structure, dy, x; write dvals, dx"))
+    return out
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--case", default="all", choices=["all", "layernorm", "scan", "spmv"])
+    ap.add_argument("--iters", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ns = ap.parse_args(argv)
+    import torch
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    time_us = _timer(dev, ns.iters, ns.warmup)
+    cases = {"layernorm": layernorm, "scan": scan, "spmv": spmv}
+    rows = []
+    for name in (cases if ns.case == "all" else [ns.case]):
+        for case, what, t, nbytes, detail in cases[name](dev, time_us):
+            gbs = nbytes / (t * 1e-6) / 1e9
+            rec = {"case": case, "entry": what, "us": round(t, 2), "bytes": nbytes,
+                   "gbs": round(gbs, 1), "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1),
+                   "bytes_are": detail}
+            print(json.dumps(rec), flush=True)
+            rows.append(rec)
+    print("\n| case | entry | event µs | algorithmic bytes | GB/s | % of 8 TB/s |")
+    print("|---|---|---:|---:|---:|---:|")
+    for r in rows:
+        print(f"| {r['case']} | {r['entry']} | {r['us']:.2f} | {r['bytes']:,} | {r['gbs']:.0f} | "
+              f"{r['pct_hbm']:.1f} |")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
