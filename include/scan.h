@@ -32,7 +32,11 @@ extern "C" {
 #endif
 
 /* Workspace bytes any scan_* call below needs for [rows, D] (0 when every
- * row fits one chunk). */
+ * row fits one chunk).  The workspace must be zero-filled once, before its
+ * first use, and kept between calls: each call leaves it zeroed again (a
+ * call is a single kernel launch, with no reset pass).  Calls that share a
+ * workspace must not overlap in time; calls on different streams need
+ * different workspaces.  A larger workspace serves smaller shapes too. */
 size_t scan_workspace_bytes(int64_t rows, int64_t D);
 
 /* float32 -> float32 inclusive scan (scan.cu:83-95, `scan_forward`). */

@@ -27,8 +27,13 @@
 //    carry, so there is no serial chain; sums are deterministic.  The grid
 //    is capped so that every workgroup is resident, and each workgroup walks
 //    its chunks in increasing order and publishes before it waits, so the
-//    lowest unpublished chunk can always make progress.  The workspace slots
-//    are reset by scan_reset_kernel (a kernel, not a memset) before each use.
+//    lowest unpublished chunk can always make progress.
+//  * The workspace cleans itself, so a call is a single launch: a slot holds
+//    its value XOR a bit pattern no total ever has, so an all-zero slot reads
+//    as "not yet published"; once every chunk of a row has read its carry
+//    (a per-row counter in the workspace), the last one zeroes the row's
+//    slots and the counter.  The caller zero-fills a workspace once, before
+//    its first use, and keeps it between calls.
 //  * Reverse scans mirror the positions: logical p <-> physical D - 1 - p.
 #include <algorithm>
 #include <cstdint>
@@ -54,22 +59,27 @@ constexpr unsigned kSpinLimit = 1u << 24;       // hang guard for the carry wait
 // ------------------------------------------------ 64-bit accumulator helpers
 template <typename Acc>
 struct Slot;
+// A published slot holds the total's bits XOR kMask; kMask itself is a bit
+// pattern no total has, so the stored word is never 0 and 0 means "empty".
 template <>
 struct Slot<double> {
   // No double computed from float inputs has all 52 mantissa bits set.
-  static constexpr unsigned long long kEmpty = ~0ull;
+  static constexpr unsigned long long kMask = ~0ull;
   __device__ static unsigned long long enc(double v) {
-    const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
-    return b == kEmpty ? 0x7FF8000000000000ull : b;
+    unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+    if (b == kMask) b = 0x7FF8000000000000ull;  // a NaN with that payload: canonical NaN
+    return b ^ kMask;
   }
-  __device__ static double dec(unsigned long long b) { return __builtin_bit_cast(double, b); }
+  __device__ static double dec(unsigned long long w) {
+    return __builtin_bit_cast(double, w ^ kMask);
+  }
 };
 template <>
 struct Slot<int64_t> {
   // |sum| <= D * 2^31 <= 2^62, so INT64_MIN never occurs.
-  static constexpr unsigned long long kEmpty = 0x8000000000000000ull;
-  __device__ static unsigned long long enc(int64_t v) { return (unsigned long long)v; }
-  __device__ static int64_t dec(unsigned long long b) { return (int64_t)b; }
+  static constexpr unsigned long long kMask = 0x8000000000000000ull;
+  __device__ static unsigned long long enc(int64_t v) { return (unsigned long long)v ^ kMask; }
+  __device__ static int64_t dec(unsigned long long w) { return (int64_t)(w ^ kMask); }
 };
 
 template <typename T>
@@ -229,7 +239,7 @@ __device__ Acc carry_in(const unsigned long long* __restrict__ slots, int chunk,
       unsigned long long b =
           __hip_atomic_load(slots + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       unsigned spins = 0;
-      while (b == Slot<Acc>::kEmpty) {
+      while (b == 0ull) {
         if (++spins > kSpinLimit) {  // never expected: report and give up
           __hip_atomic_fetch_add(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           b = Slot<Acc>::enc((Acc)0);
@@ -248,7 +258,8 @@ __device__ Acc carry_in(const unsigned long long* __restrict__ slots, int chunk,
 template <typename In, typename Out, typename Acc, bool REV, bool VEC>
 __global__ __launch_bounds__(kThreads, 4) void scan_rows_kernel(
     const In* __restrict__ x, Out* __restrict__ y, int64_t D, int nchunk, int tiles,
-    int64_t total_chunks, unsigned long long* __restrict__ slots, unsigned* __restrict__ err) {
+    int64_t total_chunks, unsigned long long* __restrict__ slots,
+    unsigned* __restrict__ row_done, unsigned* __restrict__ err) {
   __shared__ Acc s_wave[2][4];
   __shared__ Acc s_carry;
   const int lane = threadIdx.x & 63;
@@ -298,8 +309,24 @@ __global__ __launch_bounds__(kThreads, 4) void scan_rows_kernel(
         if (lane == 0 && chunk + 1 < nchunk)
           __hip_atomic_store(row_slots + chunk, Slot<Acc>::enc(chunk_total), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
+        // The publish must be visible before this chunk counts itself done
+        // (the last counter update zeroes the row's slots): wait for the
+        // store's acknowledgement (vmcnt(0) also counts stores here).
+        __builtin_amdgcn_s_waitcnt(0x0F70);
         const Acc c = carry_in<Acc>(row_slots, chunk, lane, err);
         if (lane == 0) s_carry = c;
+        // Every chunk of the row reads its carry once; the last to do so
+        // zeroes the row's slots (and the counter) for the next call.
+        unsigned prev = 0;
+        if (lane == 0)
+          prev = __hip_atomic_fetch_add(row_done + row, 1u, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+        if (__shfl(prev, 0, 64) == (unsigned)nchunk - 1) {
+          for (int p = lane; p < nchunk - 1; p += 64)
+            __hip_atomic_store(row_slots + p, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (lane == 0)
+            __hip_atomic_store(row_done + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
       __syncthreads();
       carry = s_carry;
@@ -332,16 +359,6 @@ __global__ __launch_bounds__(kThreads, 4) void scan_rows_kernel(
   }
 }
 
-// Marks every chunk slot empty and clears the hang-guard counter.
-__global__ __launch_bounds__(kThreads) void scan_reset_kernel(unsigned long long* __restrict__ slots,
-                                                              int64_t n, unsigned long long empty,
-                                                              unsigned* __restrict__ err) {
-  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * kThreads)
-    slots[i] = empty;
-  if (blockIdx.x == 0 && threadIdx.x == 0) *err = 0u;
-}
-
 // ----------------------------------------------------------------- planning
 struct Plan {
   int nchunk = 1;
@@ -360,9 +377,9 @@ Plan plan(int64_t rows, int64_t D) {
   return p;
 }
 
-size_t workspace_bytes(const Plan& p) {
-  // slots, then one 8-byte word holding the hang-guard counter
-  return p.slots > 0 ? (size_t)(p.slots + 1) * 8 : 0;
+size_t workspace_bytes(const Plan& p, int64_t rows) {
+  // slots, one 4-byte counter per row, one 8-byte word (hang-guard counter)
+  return p.slots > 0 ? (size_t)p.slots * 8 + (size_t)nl2k::ceil_div(rows, 2) * 8 + 8 : 0;
 }
 
 int validate(int64_t rows, int64_t D, const char* who) {
@@ -384,21 +401,18 @@ int run(const In* x, Out* y, int64_t rows, int64_t D, void* workspace, size_t ws
   if (!x || !y) return nl2k::fail(NL2K_ERR_NULL, "%s: null pointer argument", who);
   const Plan p = plan(rows, D);
   unsigned long long* slots = nullptr;
+  unsigned* row_done = nullptr;
   unsigned* err = nullptr;
   if (p.slots > 0) {
-    const size_t need = workspace_bytes(p);
+    const size_t need = workspace_bytes(p, rows);
     if (!workspace || ws_bytes < need)
       return nl2k::fail(NL2K_ERR_WORKSPACE, "%s: workspace of %zu bytes required, got %zu", who,
                         need, workspace ? ws_bytes : (size_t)0);
     if ((reinterpret_cast<uintptr_t>(workspace) & 7u) != 0)
       return nl2k::fail(NL2K_ERR_ALIGN, "%s: workspace must be 8-byte aligned", who);
     slots = static_cast<unsigned long long*>(workspace);
-    err = reinterpret_cast<unsigned*>(slots + p.slots);
-    const int rb = (int)std::min<int64_t>(nl2k::ceil_div(p.slots, kThreads), 1024);
-    hipLaunchKernelGGL(scan_reset_kernel, dim3(rb), dim3(kThreads), 0, stream, slots, p.slots,
-                       Slot<Acc>::kEmpty, err);
-    st = nl2k::check_launch(who);
-    if (st) return st;
+    row_done = reinterpret_cast<unsigned*>(slots + p.slots);
+    err = row_done + nl2k::ceil_div(rows, 2) * 2;
   }
   const bool vec = D % 4 == 0 && nl2k::aligned16(x) && nl2k::aligned16(y);
   // Single-chunk rows never wait, so their grid is not capped.
@@ -407,11 +421,11 @@ int run(const In* x, Out* y, int64_t rows, int64_t D, void* workspace, size_t ws
   if (vec)
     hipLaunchKernelGGL((scan_rows_kernel<In, Out, Acc, REV, true>), dim3((unsigned)grid),
                        dim3(kThreads), 0, stream, x, y, D, p.nchunk, p.tiles, p.total, slots,
-                       err);
+                       row_done, err);
   else
     hipLaunchKernelGGL((scan_rows_kernel<In, Out, Acc, REV, false>), dim3((unsigned)grid),
                        dim3(kThreads), 0, stream, x, y, D, p.nchunk, p.tiles, p.total, slots,
-                       err);
+                       row_done, err);
   return nl2k::check_launch(who);
 }
 
@@ -423,7 +437,7 @@ const char* scan_last_error(void) { return nl2k::error_slot().text; }
 
 size_t scan_workspace_bytes(int64_t rows, int64_t D) {
   if (validate(rows, D, "scan_workspace_bytes")) return 0;
-  return workspace_bytes(plan(rows, D));
+  return workspace_bytes(plan(rows, D), rows);
 }
 
 int scan_forward_f32(const float* x, float* y, int64_t rows, int64_t D, void* workspace,

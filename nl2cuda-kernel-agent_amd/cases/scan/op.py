@@ -44,16 +44,31 @@ def _check(x, what, dtypes):
     capi.require(x.size(1) > 0, f"{what} expects a non-empty last dimension")
 
 
+_WORKSPACES = {}
+
+
+def _workspace(device, stream, nbytes):
+    """The zero-initialised workspace kept for (device, stream): the kernels
+    leave it zeroed after every call, so it is allocated (and zeroed) only
+    when a larger one is needed."""
+    key = (device.index, stream.value)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() * 8 < nbytes:
+        ws = torch.zeros(max((nbytes + 7) // 8, 1), dtype=torch.int64, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
 def _call(fn_name, x, out_dtype, what):
     lib = _lib()
     x = x.contiguous()
     rows, d = x.shape
     y = torch.empty((rows, d), dtype=out_dtype, device=x.device)
     ws_bytes = lib.scan_workspace_bytes(rows, d)
-    ws = torch.empty(max(ws_bytes // 8, 1), dtype=torch.int64, device=x.device)
+    ws = _workspace(x.device, capi.stream_of(x), ws_bytes)
     with torch.cuda.device(x.device):
-        st = getattr(lib, fn_name)(capi.ptr(x), capi.ptr(y), rows, d, capi.ptr(ws), ws_bytes,
-                                   capi.stream_of(x))
+        st = getattr(lib, fn_name)(capi.ptr(x), capi.ptr(y), rows, d, capi.ptr(ws),
+                                   ws.numel() * 8, capi.stream_of(x))
     capi.check(st, lib.scan_last_error, what)
     return y
 

@@ -101,7 +101,7 @@ def scan(dev, time_us):
         y64 = torch.empty(R, D, dtype=torch.int64, device=dev)
         y32 = torch.empty_like(xi)
         wsb = lib.scan_workspace_bytes(R, D)
-        ws = torch.empty(max(wsb // 8, 1), dtype=torch.int64, device=dev)
+        ws = torch.zeros(max(wsb // 8, 1), dtype=torch.int64, device=dev)  # zeroed once
         s, P = capi.stream_of(x), capi.ptr
         shape = f"[{R},{D}]"
         for name, fn, nbytes, what in (

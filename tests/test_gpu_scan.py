@@ -144,17 +144,19 @@ def test_scan_full_size_identities():
     rowsum = x.double().sum(dim=1).float()
     assert torch.allclose(y1[:, -1], rowsum, atol=1e-3, rtol=1e-3)
     assert torch.allclose(rb[:, 0], rowsum, atol=1e-3, rtol=1e-3)
-    # direct C-ABI call; the word after the chunk slots counts guard trips
+    # direct C-ABI calls on a fresh zeroed workspace: every call leaves it
+    # zeroed again (slots and per-row counters; the last word counts
+    # hang-guard trips, which must stay 0)
     rows, d = x.shape
     nbytes = lib.scan_workspace_bytes(rows, d)
-    ws = torch.empty(nbytes // 8, dtype=torch.int64, device="cuda")
-    y3 = torch.empty_like(x)
-    st = lib.scan_forward_f32(capi.ptr(x), capi.ptr(y3), rows, d, capi.ptr(ws), nbytes,
-                              capi.stream_of(x))
-    assert st == 0, lib.scan_last_error()
-    torch.cuda.synchronize()
-    assert torch.equal(y3, y1)
-    assert int(ws[-1].item()) & 0xFFFFFFFF == 0
+    ws = torch.zeros(nbytes // 8, dtype=torch.int64, device="cuda")
+    for fn in (lib.scan_forward_f32, lib.scan_backward_f32, lib.scan_forward_f32):
+        y3 = torch.empty_like(x)
+        st = fn(capi.ptr(x), capi.ptr(y3), rows, d, capi.ptr(ws), nbytes, capi.stream_of(x))
+        assert st == 0, lib.scan_last_error()
+        torch.cuda.synchronize()
+        assert torch.equal(y3, y1 if fn is lib.scan_forward_f32 else rb)
+        assert int(torch.count_nonzero(ws)) == 0, "workspace not left zeroed"
 
 
 def test_scan_verify_all_reference_defaults():
