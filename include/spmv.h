@@ -12,9 +12,9 @@
  * on the structure (row_ptr[0] = 0, non-decreasing, row_ptr[M] = nnz,
  * 0 <= col_idx < K) cannot be checked without reading device memory; the
  * kernels clamp every index they load into range, so a malformed structure
- * gives wrong numbers, never an out-of-bounds access.  The forward is
- * deterministic; dX is accumulated with fp32 atomics (order varies between
- * runs, as in the reference).
+ * gives wrong numbers, never an out-of-bounds access.  The forward and
+ * dvals are deterministic; the order of the additions into each dX element
+ * varies between runs (as with the reference's atomics).
  *
  * Reference interface replaced: the pybind entries `spmv_forward(row_ptr,
  * col_idx, vals, X) -> Y` and `spmv_backward(row_ptr, col_idx, vals, X,
@@ -43,15 +43,24 @@ int spmv_forward_f32_i64(const int64_t* row_ptr, const int64_t* col_idx, const f
                          const float* X, float* Y, int64_t M, int64_t K, int64_t D,
                          int64_t nnz, hipStream_t stream);
 
+/* Workspace bytes spmv_backward_f32_* needs when dX is requested (0 when
+ * none is needed: D > 1, nnz == 0, or more than 16.7M columns, where dX is
+ * accumulated with fp32 atomics instead).  The workspace is scratch: no
+ * initial contents, nothing kept; 256-byte aligned. */
+size_t spmv_backward_workspace_bytes(int64_t M, int64_t K, int64_t D, int64_t nnz);
+
 /* dvals [nnz] and dX [K, D] from dY [M, D] (spmv.cu:241-288,
  * `spmv_backward`).  Either output may be NULL to skip it; dX is fully
- * written (zeroed, then accumulated). */
+ * written.  At D == 1, dX = A^T dY is summed by column bucket in a
+ * workspace of spmv_backward_workspace_bytes() bytes (see there). */
 int spmv_backward_f32_i32(const int32_t* row_ptr, const int32_t* col_idx, const float* vals,
                           const float* X, const float* dY, float* dvals, float* dX,
-                          int64_t M, int64_t K, int64_t D, int64_t nnz, hipStream_t stream);
+                          int64_t M, int64_t K, int64_t D, int64_t nnz, void* workspace,
+                          size_t workspace_bytes, hipStream_t stream);
 int spmv_backward_f32_i64(const int64_t* row_ptr, const int64_t* col_idx, const float* vals,
                           const float* X, const float* dY, float* dvals, float* dX,
-                          int64_t M, int64_t K, int64_t D, int64_t nnz, hipStream_t stream);
+                          int64_t M, int64_t K, int64_t D, int64_t nnz, void* workspace,
+                          size_t workspace_bytes, hipStream_t stream);
 
 const char* spmv_last_error(void);
 

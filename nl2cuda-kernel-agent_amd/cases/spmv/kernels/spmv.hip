@@ -22,8 +22,19 @@
 //    is written once; the row still open at the end of the step is carried
 //    in registers.  Empty rows are written as 0 by whoever sees the gap.
 //  * D == 1 backward: the same walk gives each position its row; the wave
-//    writes dvals with 16-byte stores and adds vals * dy into dX with fp32
-//    atomics (dX zeroed first by a fill kernel).
+//    writes dvals and the contribution vals[p] * dy[row(p)] of every
+//    position with 16-byte stores, in position order.  dX = A^T dy is then
+//    a sum by column without atomics (random 4-byte atomics or stores run at
+//    the L2's request rate, ~20 G/s and ~170 G/s here, far below streaming):
+//    a sort kernel reads tiles of 16384 positions (contribution and column),
+//    counts them per column bucket (2^k columns, about 256 buckets) in LDS,
+//    orders the tile by bucket in LDS and writes it back in place with the
+//    low column bits beside it, plus each bucket's segment offsets; one
+//    workgroup per bucket then sums its segments of every tile into an LDS
+//    copy of its dX slice (compare-and-swap float adds) and writes the slice
+//    once.  The order of the additions within a column varies between runs,
+//    as with the reference's atomics.  Column counts too large for 1024 buckets of
+//    16384 columns fall back to zero-fill plus fp32 atomics.
 //  * D > 1 (SpMM): L lanes per row (L = 4, 16 or 64), float4 columns when
 //    D % 4 == 0 and X / Y are 16-byte aligned; the lanes of a row share each
 //    (col, val) load and read the X row coalesced.  Backward: per nonzero a
@@ -44,7 +55,7 @@ typedef long long i64x2_t __attribute__((ext_vector_type(2)));
 constexpr int kThreads = 256;
 constexpr int kPer = 4;                 // positions per lane per step
 constexpr int kStep = 64 * kPer;        // positions per wave step
-constexpr int kBnd = 256;               // row starts staged per step
+constexpr int kWin = 512;               // row starts staged per LDS window (per wave)
 constexpr int64_t kWaveItems = 4096;    // rows + nonzeros per wave (D == 1)
 
 template <typename I>
@@ -80,52 +91,87 @@ __device__ int64_t rows_lower_bound(const I* __restrict__ ptr, int64_t M, int64_
   return min(lo + c, M);
 }
 
-// Loads the four col / vals entries of positions p..p+3 (p % 4 == 0 when
-// VEC); in[j] tells whether position p + j lies in [lo, hi) (entries outside
-// read as column 0 / value 0 and must not be used).
+// The raw col_idx / vals entries of positions q0..q0+3 (q0 % 4 == 0),
+// loaded without branches (a load under a branch makes the compiler wait for
+// it before the branch joins, which serialises the walk).  The vector form
+// reads 16 bytes of each array at q0 clamped to [0, nnz_full - 4], where
+// nnz_full = nnz rounded down to a multiple of 4; a wave takes it only when
+// all its positions lie below nnz_full, so no entry it uses is clamped.  The
+// scalar form reads each entry at its position clamped to [0, nnz - 1].
 template <typename I, bool VEC>
-__device__ __forceinline__ void load_quad(const I* __restrict__ col, const float* __restrict__ vals,
-                                          int64_t p, int64_t lo, int64_t hi, int64_t nnz,
-                                          int64_t K, int64_t (&c)[4], float (&v)[4],
-                                          bool (&in)[4]) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) in[j] = p + j >= lo && p + j < hi;
-  if (VEC && p + 3 < nnz && p >= 0) {
-    f32x4 vv = *reinterpret_cast<const f32x4*>(vals + p);
-    int64_t cc[4];
-    if constexpr (sizeof(I) == 4) {
-      const i32x4_t ci = *reinterpret_cast<const i32x4_t*>(col + p);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) cc[j] = ci[j];
-    } else {
-      const i64x2_t c0 = *reinterpret_cast<const i64x2_t*>(col + p);
-      const i64x2_t c1 = *reinterpret_cast<const i64x2_t*>(col + p + 2);
-      cc[0] = c0[0]; cc[1] = c0[1]; cc[2] = c1[0]; cc[3] = c1[1];
-    }
+struct Quad {
+  I c[4];
+  float v[4];
+  __device__ void issue(const I* __restrict__ col, const float* __restrict__ vals, int64_t q0,
+                        int64_t nnz) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      c[j] = in[j] ? (cc[j] < 0 ? 0 : (cc[j] >= K ? K - 1 : cc[j])) : 0;
-      v[j] = in[j] ? vv[j] : 0.f;
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t q = p + j;
-      const int64_t qc = q < 0 ? 0 : (q >= nnz ? nnz - 1 : q);
-      const int64_t cj = nnz > 0 ? ld_col(col, qc, K) : 0;
-      const float vj = nnz > 0 ? vals[qc] : 0.f;
-      c[j] = in[j] ? cj : 0;
-      v[j] = in[j] ? vj : 0.f;
+      const int64_t q = max((int64_t)0, min(q0 + j, nnz - 1));
+      c[j] = col[q];
+      v[j] = vals[q];
     }
   }
+  __device__ int64_t col_at(int j) const { return (int64_t)c[j]; }
+  __device__ float val_at(int j) const { return v[j]; }
+};
+template <>
+struct Quad<int32_t, true> {
+  i32x4_t c;
+  f32x4 v;
+  __device__ void issue(const int32_t* __restrict__ col, const float* __restrict__ vals,
+                        int64_t q0, int64_t nnz) {
+    const int64_t q = max((int64_t)0, min(q0, (nnz & ~(int64_t)3) - 4));
+    c = *reinterpret_cast<const i32x4_t*>(col + q);
+    v = *reinterpret_cast<const f32x4*>(vals + q);
+  }
+  __device__ int64_t col_at(int j) const { return (int64_t)c[j]; }
+  __device__ float val_at(int j) const { return v[j]; }
+};
+template <>
+struct Quad<int64_t, true> {
+  i64x2_t c0, c1;
+  f32x4 v;
+  __device__ void issue(const int64_t* __restrict__ col, const float* __restrict__ vals,
+                        int64_t q0, int64_t nnz) {
+    const int64_t q = max((int64_t)0, min(q0, (nnz & ~(int64_t)3) - 4));
+    c0 = *reinterpret_cast<const i64x2_t*>(col + q);
+    c1 = *reinterpret_cast<const i64x2_t*>(col + q + 2);
+    v = *reinterpret_cast<const f32x4*>(vals + q);
+  }
+  __device__ int64_t col_at(int j) const { return j < 2 ? c0[j] : c1[j - 2]; }
+  __device__ float val_at(int j) const { return v[j]; }
+};
+
+// Columns (clamped into [0, K)) and values of positions q0..q0+3; in[j]
+// tells whether q0 + j lies in [lo, hi); entries outside read as column 0,
+// value 0.
+template <typename Q>
+__device__ __forceinline__ void quad_get(const Q& qd, int64_t K, int64_t q0, int64_t lo,
+                                         int64_t hi, int64_t (&c)[4], float (&v)[4],
+                                         bool (&in)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    in[j] = q0 + j >= lo && q0 + j < hi;
+    const int64_t cj = qd.col_at(j);
+    c[j] = in[j] ? (cj < 0 ? 0 : (cj >= K ? K - 1 : cj)) : 0;
+    v[j] = in[j] ? qd.val_at(j) : 0.f;
+  }
+}
+
+__device__ __forceinline__ int64_t readlane64(int64_t v, int l) {
+  const unsigned lo = __builtin_amdgcn_readlane((int)(unsigned)(uint64_t)v, l);
+  const unsigned hi = __builtin_amdgcn_readlane((int)(unsigned)((uint64_t)v >> 32), l);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
 // One wave's row range and the state of its walk over the nonzeros.
 struct Walk {
   int64_t r0, r1;       // owned rows [r0, r1)
-  int64_t b;            // row_ptr[r1]
+  int64_t b;            // row_ptr[r1]: end of the owned nonzeros
   int64_t pos;          // first unprocessed nonzero
-  int64_t carry_row;    // row still open (its nonzeros before pos are summed)
+  int64_t carry_row;    // row still open (its nonzeros before pos are done)
+  int64_t wr;           // LDS window: bnd[k] = start of row wr + 1 + k
+  int64_t wlimit;       // start of row wr + kWin: positions below it resolve
 };
 
 template <typename I>
@@ -140,113 +186,114 @@ __device__ __forceinline__ bool walk_begin(const I* __restrict__ ptr, int64_t M,
   return true;
 }
 
-// Stages the starts of rows carry_row + 1 .. carry_row + kBnd relative to
-// pos (clamped to [-1, kStep + 1]; rows >= r1 start at b) into `bnd` and
-// returns the absolute start of row carry_row + kBnd.
+// Stages the starts of rows carry_row + 1 .. carry_row + kWin (absolute;
+// rows >= r1 read as b) into the wave's LDS window.  The row_ptr loads are
+// unconditional (row index clamped to r1 <= M).
 template <typename I>
-__device__ __forceinline__ int64_t stage_bounds(const I* __restrict__ ptr, int64_t nnz,
-                                                const Walk& s, int lane, int* bnd) {
+__device__ __forceinline__ void stage_window(const I* __restrict__ ptr, int64_t nnz, Walk& s,
+                                             int lane, int64_t* bnd) {
+  int64_t v[kWin / 64];
+#pragma unroll
+  for (int i = 0; i < kWin / 64; ++i) {  // all loads first, then the LDS writes
+    const int64_t r = s.carry_row + 1 + lane + 64 * i;
+    v[i] = (int64_t)ptr[min(r, s.r1)];
+  }
+  __builtin_amdgcn_wave_barrier();  // every lane is done reading the old window
   int64_t last = 0;
 #pragma unroll
-  for (int i = 0; i < kBnd / 64; ++i) {
-    const int k = lane + 64 * i;
-    const int64_t r = s.carry_row + 1 + k;
-    const int64_t v = r < s.r1 ? ld_ptr(ptr, r, nnz) : s.b;
-    const int64_t rel = v - s.pos;
-    bnd[k] = (int)(rel < -1 ? -1 : (rel > kStep + 1 ? kStep + 1 : rel));
-    last = v;
+  for (int i = 0; i < kWin / 64; ++i) {
+    const int64_t r = s.carry_row + 1 + lane + 64 * i;
+    last = r < s.r1 ? min(max(v[i], (int64_t)0), nnz) : s.b;
+    bnd[lane + 64 * i] = last;
   }
   __builtin_amdgcn_wave_barrier();
-  const unsigned lo = __builtin_amdgcn_readlane((int)(unsigned)(uint64_t)last, 63);
-  const unsigned hi = __builtin_amdgcn_readlane((int)(unsigned)((uint64_t)last >> 32), 63);
-  return (int64_t)(((uint64_t)hi << 32) | lo);
+  s.wr = s.carry_row;
+  s.wlimit = readlane64(last, 63);
 }
 
-// Rows of this lane's four positions q0..q0+3, each clamped into
-// [pos, step_end - 1]: carry_row + #{k : bnd[k] <= q - pos}.
-__device__ __forceinline__ void position_rows(const int* bnd, int64_t carry_row, int off0,
-                                              int off_max, int64_t (&rid)[4]) {
-  int off = max(0, min(off0, off_max));
+// Rows of positions q0..q0+3, each clamped into [pos, qmax]:
+// wr + #{k : bnd[k] <= q}, kept inside [r0, r1 - 1].
+__device__ __forceinline__ void window_rows(const int64_t* bnd, const Walk& s, int64_t q0,
+                                            int64_t qmax, int64_t (&rid)[4]) {
+  int64_t q = max(s.pos, min(q0, qmax));
   int idx = 0;
 #pragma unroll
-  for (int s = kBnd / 2; s >= 1; s >>= 1)
-    if (bnd[idx + s - 1] <= off) idx += s;
-  rid[0] = carry_row + idx;
+  for (int st = kWin / 2; st >= 1; st >>= 1)
+    if (bnd[idx + st - 1] <= q) idx += st;
+  rid[0] = min(s.wr + idx, s.r1 - 1);
 #pragma unroll
   for (int j = 1; j < 4; ++j) {
-    off = max(0, min(off0 + j, off_max));
-    while (idx < kBnd - 1 && bnd[idx] <= off) ++idx;
-    rid[j] = carry_row + idx;
+    q = max(s.pos, min(q0 + j, qmax));
+    while (idx < kWin - 1 && bnd[idx] <= q) ++idx;
+    rid[j] = min(s.wr + idx, s.r1 - 1);
   }
 }
 
 // ------------------------------------------------------------ D == 1 forward
 template <typename I, bool VEC>
-__global__ __launch_bounds__(kThreads) void spmv_d1_fwd_kernel(
-    const I* __restrict__ ptr, const I* __restrict__ col, const float* __restrict__ vals,
-    const float* __restrict__ x, float* __restrict__ y, int64_t M, int64_t K, int64_t nnz,
-    int64_t n_waves) {
-  __shared__ int bnd_s[kThreads / 64][kBnd];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int64_t w = (int64_t)blockIdx.x * (kThreads / 64) + wave;
-  if (w >= n_waves) return;  // wave-uniform; the kernel has no workgroup barrier
-  int* bnd = bnd_s[wave];
-  Walk s;
-  if (!walk_begin(ptr, M, nnz, w, n_waves, lane, s)) return;
+__device__ __forceinline__ void fwd_walk(const I* __restrict__ ptr, const I* __restrict__ col,
+                                         const float* __restrict__ vals,
+                                         const float* __restrict__ x, float* __restrict__ y,
+                                         int64_t K, int64_t nnz, Walk& s, int lane,
+                                         int64_t* bnd) {
   float carry_val = 0.f;
+  stage_window(ptr, nnz, s, lane, bnd);
+  Quad<I, VEC> cur;
+  if (s.pos < s.b) cur.issue(col, vals, (s.pos & ~(int64_t)3) + kPer * lane, nnz);
 
   while (s.pos < s.b) {
-    const int64_t last = stage_bounds(ptr, nnz, s, lane, bnd);
-    if (last <= s.pos) {
-      // kBnd or more rows start at or before pos: all but carry_row are empty.
-      if (lane == 0) y[s.carry_row] = carry_val;
-      for (int k = lane; k < kBnd - 1; k += 64) y[s.carry_row + 1 + k] = 0.f;
-      s.carry_row += kBnd;
-      carry_val = 0.f;
-      __builtin_amdgcn_wave_barrier();
-      continue;
-    }
     const int64_t base = s.pos & ~(int64_t)3;
-    const int64_t step_end = min(min(base + kStep, s.b), last);
+    const int64_t want = min(base + kStep, s.b);
+    if (s.wlimit < want && s.wr != s.carry_row) stage_window(ptr, nnz, s, lane, bnd);
+    if (s.wlimit <= s.pos) {
+      // Rows carry_row .. carry_row + kWin - 1 all end at or before pos.
+      if (lane == 0) y[s.carry_row] = carry_val;
+      for (int k = lane; k < kWin - 1; k += 64) y[s.carry_row + 1 + k] = 0.f;
+      s.carry_row += kWin;
+      carry_val = 0.f;
+      continue;  // restaged next iteration (wr != carry_row)
+    }
+    const int64_t step_end = min(want, s.wlimit);
     const int64_t q0 = base + kPer * lane;
     int64_t c[4];
     float v[4];
     bool in[4];
-    load_quad<I, VEC>(col, vals, q0, s.pos, step_end, nnz, K, c, v, in);
+    quad_get(cur, K, q0, s.pos, step_end, c, v, in);
+    float xv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xv[j] = x[c[j]];
+    Quad<I, VEC> nxt;  // the next step starts at step_end
+    nxt.issue(col, vals, (step_end & ~(int64_t)3) + kPer * lane, nnz);
     int64_t rid[4];
-    position_rows(bnd, s.carry_row, (int)(q0 - s.pos), (int)(step_end - 1 - s.pos), rid);
+    window_rows(bnd, s, q0, step_end - 1, rid);
     float pr[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float xv = x[c[j]];
-      pr[j] = in[j] ? v[j] * xv : 0.f;
-    }
+    for (int j = 0; j < 4; ++j) pr[j] = in[j] ? v[j] * xv[j] : 0.f;
 
     // Lane-local segments: first (kf, sf), last (kl, sl); middle rows are
     // complete and written here, as are empty rows in the gaps.
-    int64_t cur = rid[0];
+    int64_t cur_row = rid[0];
     float acc = pr[0];
-    int64_t kf = cur;
+    int64_t kf = cur_row;
     float sf = 0.f;
     bool single = true;
 #pragma unroll
     for (int j = 1; j < 4; ++j) {
-      if (rid[j] == cur) {
+      if (rid[j] == cur_row) {
         acc += pr[j];
       } else {
         if (single) {
           sf = acc;
           single = false;
         } else {
-          y[cur] = acc;
+          y[cur_row] = acc;
         }
-        for (int64_t r = cur + 1; r < rid[j]; ++r) y[r] = 0.f;
-        cur = rid[j];
+        for (int64_t r = cur_row + 1; r < rid[j]; ++r) y[r] = 0.f;
+        cur_row = rid[j];
         acc = pr[j];
       }
     }
-    const int64_t kl = cur;
+    const int64_t kl = cur_row;
     const float sl = acc;
     if (single) sf = acc;
 
@@ -279,70 +326,342 @@ __global__ __launch_bounds__(kThreads) void spmv_d1_fwd_kernel(
     carry_val = new_row == carry_row ? new_T + carry_val : new_T;
     s.carry_row = new_row;
     s.pos = step_end;
-    __builtin_amdgcn_wave_barrier();  // bnd is restaged next step
+    cur = nxt;
   }
   if (lane == 0) y[s.carry_row] = carry_val;
   for (int64_t r = s.carry_row + 1 + lane; r < s.r1; r += 64) y[r] = 0.f;
 }
 
-// ----------------------------------------------------------- D == 1 backward
 template <typename I, bool VEC>
-__global__ __launch_bounds__(kThreads) void spmv_d1_bwd_kernel(
+__global__ __launch_bounds__(kThreads) void spmv_d1_fwd_kernel(
     const I* __restrict__ ptr, const I* __restrict__ col, const float* __restrict__ vals,
-    const float* __restrict__ x, const float* __restrict__ dy, float* __restrict__ dvals,
-    float* __restrict__ dx, int64_t M, int64_t K, int64_t nnz, int64_t n_waves) {
-  __shared__ int bnd_s[kThreads / 64][kBnd];
+    const float* __restrict__ x, float* __restrict__ y, int64_t M, int64_t K, int64_t nnz,
+    int64_t n_waves) {
+  __shared__ int64_t bnd_s[kThreads / 64][kWin];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t w = (int64_t)blockIdx.x * (kThreads / 64) + wave;
-  if (w >= n_waves) return;
-  int* bnd = bnd_s[wave];
+  if (w >= n_waves) return;  // wave-uniform; the kernel has no workgroup barrier
   Walk s;
   if (!walk_begin(ptr, M, nnz, w, n_waves, lane, s)) return;
+  if constexpr (VEC) {
+    if (s.b <= (nnz & ~(int64_t)3)) {
+      fwd_walk<I, true>(ptr, col, vals, x, y, K, nnz, s, lane, bnd_s[wave]);
+      return;
+    }
+  }
+  fwd_walk<I, false>(ptr, col, vals, x, y, K, nnz, s, lane, bnd_s[wave]);
+}
 
+// ----------------------------------------------------------- D == 1 backward
+// Outputs per instantiation: dvals (DV), and for dX either nothing
+// (kNoDx), the per-position contributions vals[p] * dy[row(p)] in position
+// order (kContrib, summed by column afterwards), or fp32 atomics into a
+// zeroed dx (kAtomic, the fallback).
+constexpr int kNoDx = 0, kContrib = 1, kAtomic = 2;
+
+template <typename I, bool VEC, bool DV, int MODE>
+__device__ __forceinline__ void bwd_walk(const I* __restrict__ ptr, const I* __restrict__ col,
+                                         const float* __restrict__ vals,
+                                         const float* __restrict__ x,
+                                         const float* __restrict__ dy, float* __restrict__ dvals,
+                                         float* __restrict__ out, int64_t K, int64_t nnz,
+                                         Walk& s, int lane, int64_t* bnd) {
+  stage_window(ptr, nnz, s, lane, bnd);
+  Quad<I, VEC> cur;
+  if (s.pos < s.b) cur.issue(col, vals, (s.pos & ~(int64_t)3) + kPer * lane, nnz);
   while (s.pos < s.b) {
-    const int64_t last = stage_bounds(ptr, nnz, s, lane, bnd);
-    if (last <= s.pos) {
-      s.carry_row += kBnd;
-      __builtin_amdgcn_wave_barrier();
+    const int64_t base = s.pos & ~(int64_t)3;
+    const int64_t want = min(base + kStep, s.b);
+    if (s.wlimit < want && s.wr != s.carry_row) stage_window(ptr, nnz, s, lane, bnd);
+    if (s.wlimit <= s.pos) {
+      s.carry_row += kWin;
       continue;
     }
-    const int64_t base = s.pos & ~(int64_t)3;
-    const int64_t step_end = min(min(base + kStep, s.b), last);
+    const int64_t step_end = min(want, s.wlimit);
     const int64_t q0 = base + kPer * lane;
     int64_t c[4];
     float v[4];
     bool in[4];
-    load_quad<I, VEC>(col, vals, q0, s.pos, step_end, nnz, K, c, v, in);
+    quad_get(cur, K, q0, s.pos, step_end, c, v, in);
     int64_t rid[4];
-    position_rows(bnd, s.carry_row, (int)(q0 - s.pos), (int)(step_end - 1 - s.pos), rid);
-    float g[4], dv[4];
+    window_rows(bnd, s, q0, step_end - 1, rid);
+    float g[4], xv[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      g[j] = dy[rid[j]];
-      dv[j] = g[j] * x[c[j]];
+    for (int j = 0; j < 4; ++j) g[j] = dy[rid[j]];
+    if constexpr (DV) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xv[j] = x[c[j]];
     }
+    Quad<I, VEC> nxt;
+    nxt.issue(col, vals, (step_end & ~(int64_t)3) + kPer * lane, nnz);
     const bool full = in[0] && in[3];
-    if (dvals) {
+    if constexpr (DV) {
       if (VEC && full) {
-        *reinterpret_cast<f32x4*>(dvals + q0) = f32x4{dv[0], dv[1], dv[2], dv[3]};
+        *reinterpret_cast<f32x4*>(dvals + q0) =
+            f32x4{g[0] * xv[0], g[1] * xv[1], g[2] * xv[2], g[3] * xv[3]};
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          if (in[j]) dvals[q0 + j] = dv[j];
+          if (in[j]) dvals[q0 + j] = g[j] * xv[j];
       }
     }
-    if (dx) {
+    if constexpr (MODE == kContrib) {
+      if (VEC && full) {
+        *reinterpret_cast<f32x4*>(out + q0) =
+            f32x4{v[0] * g[0], v[1] * g[1], v[2] * g[2], v[3] * g[3]};
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (in[j]) out[q0 + j] = v[j] * g[j];
+      }
+    }
+    if constexpr (MODE == kAtomic) {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         if (in[j])
-          __hip_atomic_fetch_add(dx + c[j], v[j] * g[j], __ATOMIC_RELAXED,
+          __hip_atomic_fetch_add(out + c[j], v[j] * g[j], __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_AGENT);
     }
     s.carry_row = __shfl(rid[3], 63, 64);
     s.pos = step_end;
-    __builtin_amdgcn_wave_barrier();
+    cur = nxt;
   }
+}
+
+// `out` is the contribution array (kContrib) or dx (kAtomic).
+template <typename I, bool VEC, bool DV, int MODE>
+__global__ __launch_bounds__(kThreads) void spmv_d1_bwd_kernel(
+    const I* __restrict__ ptr, const I* __restrict__ col, const float* __restrict__ vals,
+    const float* __restrict__ x, const float* __restrict__ dy, float* __restrict__ dvals,
+    float* __restrict__ out, int64_t M, int64_t K, int64_t nnz, int64_t n_waves) {
+  __shared__ int64_t bnd_s[kThreads / 64][kWin];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t w = (int64_t)blockIdx.x * (kThreads / 64) + wave;
+  if (w >= n_waves) return;
+  Walk s;
+  if (!walk_begin(ptr, M, nnz, w, n_waves, lane, s)) return;
+  if (s.pos >= s.b) return;
+  if constexpr (VEC) {
+    if (s.b <= (nnz & ~(int64_t)3)) {
+      bwd_walk<I, true, DV, MODE>(ptr, col, vals, x, dy, dvals, out, K, nnz, s, lane,
+                                  bnd_s[wave]);
+      return;
+    }
+  }
+  bwd_walk<I, false, DV, MODE>(ptr, col, vals, x, dy, dvals, out, K, nnz, s, lane, bnd_s[wave]);
+}
+
+// -------------------------------------------- D == 1 dX: bucket sort + sum
+constexpr int kSortThreads = 512;
+constexpr int kSortTile = 16384;                    // positions per sort workgroup
+constexpr int kSortPer = kSortTile / kSortThreads;  // 32 per thread, as 8 quads
+constexpr int kMaxBuckets = 1024;
+constexpr int kMaxBucketCols = 16384;               // LDS floats of one bucket's sums
+constexpr int kSumThreads = 1024;
+constexpr int kSumWaves = kSumThreads / 64;
+constexpr int kSumUnroll = 8;
+
+// Float add into LDS through a 32-bit compare-and-swap loop.  On gfx950
+// ds_add_f32 retires about one lane per three clocks per CU whatever the
+// addresses; a read plus ds_cmpst_rtn_b32, retried only when another lane
+// changed the word in between, runs about four times faster on scattered
+// addresses.  Every failed exchange means another update succeeded, so the
+// loop ends.
+__device__ __forceinline__ void lds_add_f32(float* p, float v) {
+  unsigned* u = reinterpret_cast<unsigned*>(p);
+  unsigned old = *u;
+  while (true) {
+    const unsigned assumed = old;
+    old = atomicCAS(u, assumed, __float_as_uint(__uint_as_float(assumed) + v));
+    if (old == assumed) break;
+  }
+}
+
+__device__ __forceinline__ unsigned wave_incl_scan(unsigned v, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const unsigned u = __shfl_up(v, d, 64);
+    if (lane >= d) v += u;
+  }
+  return v;
+}
+
+// Tile t = positions [16384 t, 16384 t + 16384): reads the contributions
+// (`val`) and columns, orders the tile by bucket (column >> shift) and
+// writes it back in place -- val[lo + i] and the low column bits lowcol[lo
+// + i] -- and meta[t * (nb + 1) + b] = absolute start of bucket b's segment
+// (meta[.. + nb] = end of the tile).  The whole tile is read into
+// registers before anything is written, and tiles are disjoint, so the
+// in-place write is safe.
+template <typename I, bool VEC>
+__global__ __launch_bounds__(kSortThreads) void spmv_bucket_sort_kernel(
+    const I* __restrict__ col, float* __restrict__ val, uint16_t* __restrict__ lowcol,
+    int64_t* __restrict__ meta, int64_t nnz, int64_t K, int shift, int nb) {
+  __shared__ float s_val[kSortTile];
+  __shared__ uint16_t s_low[kSortTile];
+  __shared__ unsigned s_cur[kMaxBuckets];
+  __shared__ unsigned s_wave[kSortThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t lo = (int64_t)blockIdx.x * kSortTile;
+  const int n = (int)min((int64_t)kSortTile, nnz - lo);
+  for (int b = tid; b < nb; b += kSortThreads) s_cur[b] = 0;
+
+  unsigned cc[kSortPer];
+  float vv[kSortPer];
+#pragma unroll
+  for (int g = 0; g < kSortPer / 4; ++g) {
+    const int i = 4 * (tid + kSortThreads * g);
+    if (VEC && i + 3 < n) {
+      const f32x4 v4 = *reinterpret_cast<const f32x4*>(val + lo + i);
+      int64_t c4[4];
+      if constexpr (sizeof(I) == 4) {
+        const i32x4_t ci = *reinterpret_cast<const i32x4_t*>(col + lo + i);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c4[j] = ci[j];
+      } else {
+        const i64x2_t c0 = *reinterpret_cast<const i64x2_t*>(col + lo + i);
+        const i64x2_t c1 = *reinterpret_cast<const i64x2_t*>(col + lo + i + 2);
+        c4[0] = c0[0]; c4[1] = c0[1]; c4[2] = c1[0]; c4[3] = c1[1];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        cc[4 * g + j] = (unsigned)(c4[j] < 0 ? 0 : (c4[j] >= K ? K - 1 : c4[j]));
+        vv[4 * g + j] = v4[j];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool ok = i + j < n;
+        cc[4 * g + j] = ok ? (unsigned)ld_col(col, lo + i + j, K) : 0u;
+        vv[4 * g + j] = ok ? val[lo + i + j] : 0.f;
+      }
+    }
+  }
+  __syncthreads();  // s_cur zeroed
+#pragma unroll
+  for (int g = 0; g < kSortPer / 4; ++g)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (4 * (tid + kSortThreads * g) + j < n)
+        __hip_atomic_fetch_add(&s_cur[cc[4 * g + j] >> shift], 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
+  __syncthreads();
+
+  // Exclusive scan of the nb <= 1024 bucket counts, two per thread.
+  const int b0 = 2 * tid;
+  const unsigned a0 = b0 < nb ? s_cur[b0] : 0u;
+  const unsigned a1 = b0 + 1 < nb ? s_cur[b0 + 1] : 0u;
+  const unsigned incl = wave_incl_scan(a0 + a1, lane);
+  if (lane == 63) s_wave[wave] = incl;
+  __syncthreads();
+  unsigned off = incl - (a0 + a1);
+  for (int w = 0; w < wave; ++w) off += s_wave[w];
+  int64_t* mrow = meta + (int64_t)blockIdx.x * (nb + 1);
+  if (b0 < nb) {
+    s_cur[b0] = off;
+    mrow[b0] = lo + off;
+  }
+  if (b0 + 1 < nb) {
+    s_cur[b0 + 1] = off + a0;
+    mrow[b0 + 1] = lo + off + a0;
+  }
+  if (tid == 0) mrow[nb] = lo + n;
+  __syncthreads();
+
+  // Place: a bucket's cursor hands out the slots of its segment.
+  const unsigned low_mask = (1u << shift) - 1u;
+#pragma unroll
+  for (int g = 0; g < kSortPer / 4; ++g)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (4 * (tid + kSortThreads * g) + j < n) {
+        const unsigned c = cc[4 * g + j];
+        unsigned r = __hip_atomic_fetch_add(&s_cur[c >> shift], 1u, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_WORKGROUP);
+        r = r < (unsigned)kSortTile ? r : (unsigned)kSortTile - 1u;
+        s_val[r] = vv[4 * g + j];
+        s_low[r] = (uint16_t)(c & low_mask);
+      }
+  __syncthreads();
+
+  for (int i = 4 * tid; i < n; i += 4 * kSortThreads) {
+    if (i + 3 < n) {
+      *reinterpret_cast<f32x4*>(val + lo + i) = *reinterpret_cast<const f32x4*>(s_val + i);
+      *reinterpret_cast<uint2*>(lowcol + lo + i) = *reinterpret_cast<const uint2*>(s_low + i);
+    } else {
+      for (int j = i; j < n; ++j) {
+        val[lo + j] = s_val[j];
+        lowcol[lo + j] = s_low[j];
+      }
+    }
+  }
+}
+
+// dx[b * cols, b * cols + cols) for bucket b = blockIdx.x: the bucket's
+// segments of every tile, summed in LDS.  A wave takes 64 tiles at a time
+// and treats their segments as one list (an exclusive prefix of the segment
+// lengths in LDS maps list entry e to its tile), so each lane loads
+// kSumUnroll independent entries per round.
+__global__ __launch_bounds__(kSumThreads) void spmv_bucket_sum_kernel(
+    const float* __restrict__ val, const uint16_t* __restrict__ lowcol,
+    const int64_t* __restrict__ meta, int64_t n_tiles, int nb, int cols, int64_t K,
+    int64_t nnz, float* __restrict__ dx) {
+  __shared__ float acc[kMaxBucketCols];
+  __shared__ int64_t s_start[kSumWaves][64];
+  __shared__ int s_pre[kSumWaves][65];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = blockIdx.x;
+  for (int i = tid; i < cols; i += kSumThreads) acc[i] = 0.f;
+  __syncthreads();
+  const int64_t n_groups = (n_tiles + 63) / 64;
+  for (int64_t grp = wave; grp < n_groups; grp += kSumWaves) {
+    const int64_t t = grp * 64 + lane;
+    int64_t m0 = 0, m1 = 0;
+    if (t < n_tiles) {
+      const int64_t* m = meta + t * (nb + 1) + b;
+      m0 = min(max(m[0], (int64_t)0), nnz);
+      m1 = min(max(m[1], m0), min(nnz, m0 + kSortTile));
+    }
+    const int len = (int)(m1 - m0);
+    const int incl = (int)wave_incl_scan((unsigned)len, lane);
+    s_start[wave][lane] = m0;
+    s_pre[wave][lane] = incl - len;
+    if (lane == 63) s_pre[wave][64] = incl;
+    const int E = __shfl(incl, 63, 64);
+    __builtin_amdgcn_wave_barrier();
+    int j = 0;  // the lane's current tile; entries e grow, so j only advances
+    for (int e0 = 0; e0 < E; e0 += 64 * kSumUnroll) {
+      // Positions first (LDS only), then every global load without a branch
+      // between them, then the LDS additions.
+      int64_t pp[kSumUnroll];
+      bool ok[kSumUnroll];
+#pragma unroll
+      for (int u = 0; u < kSumUnroll; ++u) {
+        const int e = e0 + 64 * u + lane;
+        ok[u] = e < E;
+        const int ee = ok[u] ? e : E - 1;       // E - 1 >= every earlier e
+        while (s_pre[wave][j + 1] <= ee) ++j;   // stops: s_pre[wave][64] = E > ee
+        pp[u] = s_start[wave][j] + (ee - s_pre[wave][j]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      float v[kSumUnroll];
+      unsigned c[kSumUnroll];
+#pragma unroll
+      for (int u = 0; u < kSumUnroll; ++u) {
+        v[u] = val[pp[u]];
+        c[u] = lowcol[pp[u]];
+      }
+#pragma unroll
+      for (int u = 0; u < kSumUnroll; ++u)
+        if (ok[u]) lds_add_f32(&acc[c[u] & (unsigned)(cols - 1)], v[u]);
+    }
+    __builtin_amdgcn_wave_barrier();  // s_start / s_pre are rewritten next group
+  }
+  __syncthreads();
+  const int64_t c0 = (int64_t)b * cols;
+  for (int i = tid; i < cols && c0 + i < K; i += kSumThreads) dx[c0 + i] = acc[i];
 }
 
 // ------------------------------------------------------------------ D > 1
@@ -514,14 +833,103 @@ int forward(const I* ptr, const I* col, const float* vals, const float* X, float
 }
 
 template <typename I>
+void launch_d1_bwd(bool vec, bool dv, int mode, unsigned blocks, hipStream_t stream,
+                   const I* ptr, const I* col, const float* vals, const float* X,
+                   const float* dY, float* dvals, float* out, int64_t M, int64_t K,
+                   int64_t nnz, int64_t n_waves) {
+#define D1_BWD(V, DVV, MM)                                                                   \
+  hipLaunchKernelGGL((spmv_d1_bwd_kernel<I, V, DVV, MM>), dim3(blocks), dim3(kThreads), 0, \
+                     stream, ptr, col, vals, X, dY, dvals, out, M, K, nnz, n_waves)
+#define D1_BWD_MODE(V, DVV)                     \
+  if (mode == kContrib) D1_BWD(V, DVV, kContrib); \
+  else if (mode == kAtomic) D1_BWD(V, DVV, kAtomic); \
+  else D1_BWD(V, DVV, kNoDx)
+  if (vec) {
+    if (dv) { D1_BWD_MODE(true, true); } else { D1_BWD_MODE(true, false); }
+  } else {
+    if (dv) { D1_BWD_MODE(false, true); } else { D1_BWD_MODE(false, false); }
+  }
+#undef D1_BWD_MODE
+#undef D1_BWD
+}
+
+// dX by bucket sort (D == 1): bucket width `cols` = 2^shift, nb buckets,
+// n_tiles sort tiles; workspace = contributions (sorted in place) | low
+// column bits | segment offsets.
+struct BucketPlan {
+  bool use = false;
+  int shift = 0, cols = 0, nb = 0;
+  int64_t n_tiles = 0;
+  size_t off_low = 0, off_meta = 0, bytes = 0;
+};
+
+size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+BucketPlan bucket_plan(int64_t K, int64_t D, int64_t nnz) {
+  BucketPlan p;
+  if (D != 1 || nnz <= 0 || K < 1) return p;
+  int shift = 8;  // about 256 buckets, 256 .. 16384 columns each
+  while ((int64_t(1) << shift) < kMaxBucketCols && (int64_t(256) << shift) < K) ++shift;
+  const int64_t nb = nl2k::ceil_div(K, int64_t(1) << shift);
+  if (nb > kMaxBuckets) return p;
+  p.use = true;
+  p.shift = shift;
+  p.cols = 1 << shift;
+  p.nb = (int)nb;
+  p.n_tiles = nl2k::ceil_div(nnz, kSortTile);
+  p.off_low = align256((size_t)nnz * sizeof(float));
+  p.off_meta = p.off_low + align256((size_t)nnz * sizeof(uint16_t));
+  p.bytes = p.off_meta + (size_t)p.n_tiles * (size_t)(p.nb + 1) * sizeof(int64_t);
+  return p;
+}
+
+template <typename I>
 int backward(const I* ptr, const I* col, const float* vals, const float* X, const float* dY,
              float* dvals, float* dX, int64_t M, int64_t K, int64_t D, int64_t nnz,
-             hipStream_t stream, const char* who) {
+             void* workspace, size_t ws_bytes, hipStream_t stream, const char* who) {
   const int64_t imax = sizeof(I) == 4 ? INT32_MAX : INT64_MAX / 2;
   int st = validate(M, K, D, nnz, imax, who);
   if (st) return st;
   if (!ptr || !X || (M > 0 && !dY) || (nnz > 0 && (!col || !vals)))
     return nl2k::fail(NL2K_ERR_NULL, "%s: null pointer argument", who);
+  const BucketPlan bp = bucket_plan(K, D, nnz);
+  const bool sorted_dx = dX && bp.use && M > 0;
+  if (sorted_dx) {
+    if (!workspace || ws_bytes < bp.bytes)
+      return nl2k::fail(NL2K_ERR_WORKSPACE, "%s: workspace of %zu bytes required, got %zu", who,
+                        bp.bytes, workspace ? ws_bytes : (size_t)0);
+    if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+      return nl2k::fail(NL2K_ERR_ALIGN, "%s: workspace must be 256-byte aligned", who);
+  }
+  if (sorted_dx) {
+    const int64_t n_waves = std::max<int64_t>(1, nl2k::ceil_div(nnz + M, kWaveItems));
+    const int64_t blocks = nl2k::ceil_div(n_waves, kThreads / 64);
+    if (blocks > INT32_MAX || bp.n_tiles > INT32_MAX)
+      return nl2k::fail(NL2K_ERR_OVERFLOW, "%s: too many rows", who);
+    char* ws = static_cast<char*>(workspace);
+    float* contrib = reinterpret_cast<float*>(ws);
+    uint16_t* low = reinterpret_cast<uint16_t*>(ws + bp.off_low);
+    int64_t* meta = reinterpret_cast<int64_t*>(ws + bp.off_meta);
+    const bool vec = nl2k::aligned16(col) && nl2k::aligned16(vals) &&
+                     (dvals == nullptr || nl2k::aligned16(dvals));
+    launch_d1_bwd<I>(vec, dvals != nullptr, kContrib, (unsigned)blocks, stream, ptr, col, vals,
+                     X, dY, dvals, contrib, M, K, nnz, n_waves);
+    st = nl2k::check_launch(who);
+    if (st) return st;
+    if (nl2k::aligned16(col))
+      hipLaunchKernelGGL((spmv_bucket_sort_kernel<I, true>), dim3((unsigned)bp.n_tiles),
+                         dim3(kSortThreads), 0, stream, col, contrib, low, meta, nnz, K, bp.shift,
+                         bp.nb);
+    else
+      hipLaunchKernelGGL((spmv_bucket_sort_kernel<I, false>), dim3((unsigned)bp.n_tiles),
+                         dim3(kSortThreads), 0, stream, col, contrib, low, meta, nnz, K, bp.shift,
+                         bp.nb);
+    st = nl2k::check_launch(who);
+    if (st) return st;
+    hipLaunchKernelGGL(spmv_bucket_sum_kernel, dim3((unsigned)bp.nb), dim3(kSumThreads), 0,
+                       stream, contrib, low, meta, bp.n_tiles, bp.nb, bp.cols, K, nnz, dX);
+    return nl2k::check_launch(who);
+  }
   if (dX) {
     const int64_t n = K * D;
     const unsigned fb = (unsigned)std::min<int64_t>(nl2k::ceil_div(n, kThreads), 4096);
@@ -536,12 +944,8 @@ int backward(const I* ptr, const I* col, const float* vals, const float* X, cons
     if (blocks > INT32_MAX) return nl2k::fail(NL2K_ERR_OVERFLOW, "%s: too many rows", who);
     const bool vec = nl2k::aligned16(col) && nl2k::aligned16(vals) &&
                      (dvals == nullptr || nl2k::aligned16(dvals));
-    if (vec)
-      hipLaunchKernelGGL((spmv_d1_bwd_kernel<I, true>), dim3((unsigned)blocks), dim3(kThreads), 0,
-                         stream, ptr, col, vals, X, dY, dvals, dX, M, K, nnz, n_waves);
-    else
-      hipLaunchKernelGGL((spmv_d1_bwd_kernel<I, false>), dim3((unsigned)blocks), dim3(kThreads),
-                         0, stream, ptr, col, vals, X, dY, dvals, dX, M, K, nnz, n_waves);
+    launch_d1_bwd<I>(vec, dvals != nullptr, dX ? kAtomic : kNoDx, (unsigned)blocks, stream, ptr,
+                     col, vals, X, dY, dvals, dX, M, K, nnz, n_waves);
     return nl2k::check_launch(who);
   }
   const bool vec = D % 4 == 0 && nl2k::aligned16(X) && nl2k::aligned16(dY) &&
@@ -583,18 +987,25 @@ int spmv_forward_f32_i64(const int64_t* row_ptr, const int64_t* col_idx, const f
   return forward(row_ptr, col_idx, vals, X, Y, M, K, D, nnz, stream, "spmv_forward_f32_i64");
 }
 
+size_t spmv_backward_workspace_bytes(int64_t M, int64_t K, int64_t D, int64_t nnz) {
+  if (validate(M, K, D, nnz, INT64_MAX / 2, "spmv_backward_workspace_bytes")) return 0;
+  return M > 0 ? bucket_plan(K, D, nnz).bytes : 0;
+}
+
 int spmv_backward_f32_i32(const int32_t* row_ptr, const int32_t* col_idx, const float* vals,
                           const float* X, const float* dY, float* dvals, float* dX,
-                          int64_t M, int64_t K, int64_t D, int64_t nnz, hipStream_t stream) {
-  return backward(row_ptr, col_idx, vals, X, dY, dvals, dX, M, K, D, nnz, stream,
-                  "spmv_backward_f32_i32");
+                          int64_t M, int64_t K, int64_t D, int64_t nnz, void* workspace,
+                          size_t workspace_bytes, hipStream_t stream) {
+  return backward(row_ptr, col_idx, vals, X, dY, dvals, dX, M, K, D, nnz, workspace,
+                  workspace_bytes, stream, "spmv_backward_f32_i32");
 }
 
 int spmv_backward_f32_i64(const int64_t* row_ptr, const int64_t* col_idx, const float* vals,
                           const float* X, const float* dY, float* dvals, float* dX,
-                          int64_t M, int64_t K, int64_t D, int64_t nnz, hipStream_t stream) {
-  return backward(row_ptr, col_idx, vals, X, dY, dvals, dX, M, K, D, nnz, stream,
-                  "spmv_backward_f32_i64");
+                          int64_t M, int64_t K, int64_t D, int64_t nnz, void* workspace,
+                          size_t workspace_bytes, hipStream_t stream) {
+  return backward(row_ptr, col_idx, vals, X, dY, dvals, dX, M, K, D, nnz, workspace,
+                  workspace_bytes, stream, "spmv_backward_f32_i64");
 }
 
 }  // extern "C"

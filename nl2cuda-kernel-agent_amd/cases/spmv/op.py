@@ -26,7 +26,9 @@ def bind_library(lib):
     V, I64 = capi.c_void_p, capi.c_int64
     for t in ("i32", "i64"):
         capi.bind(lib, f"spmv_forward_f32_{t}", [V, V, V, V, V, I64, I64, I64, I64, V])
-        capi.bind(lib, f"spmv_backward_f32_{t}", [V, V, V, V, V, V, V, I64, I64, I64, I64, V])
+        capi.bind(lib, f"spmv_backward_f32_{t}",
+                  [V, V, V, V, V, V, V, I64, I64, I64, I64, V, capi.c_size_t, V])
+    capi.bind(lib, "spmv_backward_workspace_bytes", [I64, I64, I64, I64], restype=capi.c_size_t)
     capi.bind_last_error(lib, "spmv_last_error")
     return lib
 
@@ -82,11 +84,13 @@ def spmv_backward(row_ptr, col_idx, vals, X, grad_Y, need_vals=True, need_X=True
     K, D = X.shape
     grad_vals = torch.empty_like(vals) if need_vals else None
     grad_X = torch.empty_like(X) if need_X else None
+    ws_bytes = lib.spmv_backward_workspace_bytes(M, K, D, vals.numel()) if need_X else 0
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=X.device)  # scratch
     with torch.cuda.device(X.device):
         st = getattr(lib, f"spmv_backward_f32_{t}")(
             capi.ptr(row_ptr), capi.ptr(col_idx), capi.ptr(vals), capi.ptr(X), capi.ptr(grad_Y),
             capi.ptr(grad_vals) if need_vals else None, capi.ptr(grad_X) if need_X else None,
-            M, K, D, vals.numel(), capi.stream_of(X))
+            M, K, D, vals.numel(), capi.ptr(ws), ws_bytes, capi.stream_of(X))
     capi.check(st, lib.spmv_last_error, "spmv_backward")
     return grad_vals, grad_X
 

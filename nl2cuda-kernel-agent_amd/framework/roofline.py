@@ -130,6 +130,8 @@ def spmv(dev, time_us):
     Y = torch.empty(M, 1, device=dev)
     dY = torch.randn(M, 1, generator=torch.Generator().manual_seed(1)).to(dev)
     dv, dX = torch.empty_like(vals), torch.empty_like(X)
+    wsb = lib.spmv_backward_workspace_bytes(M, K, 1, nnz)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
     s, P = capi.stream_of(X), capi.ptr
     base = 4 * (M + 1) + 8 * nnz
     out = []
@@ -138,11 +140,13 @@ def spmv(dev, time_us):
     out.append(("spmv", "forward_f32_i32 zipf 2^20 D=1", tt, base + 4 * K + 4 * M,
                 "read row_ptr, col_idx, vals, x; write y"))
     tt = time_us(lambda: _check(lib.spmv_backward_f32_i32(P(ptr), P(col), P(vals), P(X), P(dY), None,
-                                                         P(dX), M, K, 1, nnz, s), lib, "spmv_last_error"))
+                                                         P(dX), M, K, 1, nnz, P(ws), wsb, s),
+                                lib, "spmv_last_error"))
     out.append(("spmv", "backward dx only, zipf 2^20", tt, base + 4 * M + 4 * K,
                 "read structure, dy; write dx"))
     tt = time_us(lambda: _check(lib.spmv_backward_f32_i32(P(ptr), P(col), P(vals), P(X), P(dY), P(dv),
-                                                         P(dX), M, K, 1, nnz, s), lib, "spmv_last_error"))
+                                                         P(dX), M, K, 1, nnz, P(ws), wsb, s),
+                                lib, "spmv_last_error"))
     out.append(("spmv", "backward dvals + dx, zipf 2^20", tt, base + 4 * M + 8 * K + 4 * nnz,
                 "read structure, dy, x; write dvals, dx"))
     return out
