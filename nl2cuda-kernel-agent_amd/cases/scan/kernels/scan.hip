@@ -131,33 +131,54 @@ __device__ __forceinline__ T wave_total(T v) {
 }
 
 // ------------------------------------------------------- element transport
-// Loads logical positions p..p+3 of a row as stored (zero past D).  VEC:
-// D % 4 == 0 and 16-byte aligned rows, so a group is one 16-byte load.
+// Logical positions p..p+3 of a row as stored (zero past D), in two steps so
+// that a tile's four group loads are all in flight before any is used:
+// issue() only loads (clamped address, no branch), finish() masks and
+// reverses.  Applying the mask right after each load made the compiler
+// reuse one register quad and wait for every load in turn.  VEC: D % 4 == 0
+// and 16-byte aligned rows, so a group is one 16-byte load.
 template <typename In, bool REV, bool VEC>
-__device__ __forceinline__ void load_raw(const In* __restrict__ row, int64_t D, int64_t p,
-                                         In (&a)[4]) {
-  if (VEC) {
-    const bool in = p < D;
+struct RawGroup;
+template <typename In, bool REV>
+struct RawGroup<In, REV, true> {
+  typedef In V4 __attribute__((ext_vector_type(4)));
+  V4 w;
+  __device__ __forceinline__ void issue(const In* __restrict__ row, int64_t D, int64_t p) {
     const int64_t q = REV ? D - 4 - min(p, D - 4) : min(p, D - 4);
-    In v[4];
-    if constexpr (__is_same(In, float)) {
-      const f32x4 w = *reinterpret_cast<const f32x4*>(row + q);
-      v[0] = w[0]; v[1] = w[1]; v[2] = w[2]; v[3] = w[3];
-    } else {
-      const i32x4 w = *reinterpret_cast<const i32x4*>(row + q);
-      v[0] = w[0]; v[1] = w[1]; v[2] = w[2]; v[3] = w[3];
-    }
+    w = *reinterpret_cast<const V4*>(row + q);
+  }
+  __device__ __forceinline__ void finish(int64_t D, int64_t p, In (&a)[4]) const {
+    const bool in = p < D;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) a[c] = in ? v[REV ? 3 - c : c] : (In)0;
-  } else {
+    for (int c = 0; c < 4; ++c) a[c] = in ? w[REV ? 3 - c : c] : (In)0;
+  }
+};
+template <typename In, bool REV>
+struct RawGroup<In, REV, false> {
+  In v[4];
+  __device__ __forceinline__ void issue(const In* __restrict__ row, int64_t D, int64_t p) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int64_t pc = p + c;
-      const int64_t q = REV ? D - 1 - min(pc, D - 1) : min(pc, D - 1);
-      const In v = row[q];
-      a[c] = pc < D ? v : (In)0;
+      v[c] = row[REV ? D - 1 - min(pc, D - 1) : min(pc, D - 1)];
     }
   }
+  __device__ __forceinline__ void finish(int64_t D, int64_t p, In (&a)[4]) const {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) a[c] = p + c < D ? v[c] : (In)0;
+  }
+};
+
+// The four groups of one lane in a tile: positions p0 + 256 k.
+template <typename In, bool REV, bool VEC>
+__device__ __forceinline__ void load_tile(const In* __restrict__ row, int64_t D, int64_t p0,
+                                          In (&a)[kGroups][4]) {
+  RawGroup<In, REV, VEC> g[kGroups];
+#pragma unroll
+  for (int k = 0; k < kGroups; ++k) g[k].issue(row, D, p0 + 256 * k);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int k = 0; k < kGroups; ++k) g[k].finish(D, p0 + 256 * k, a[k]);
 }
 
 template <typename Out, bool REV, bool VEC, typename Acc>
@@ -278,9 +299,7 @@ __global__ __launch_bounds__(kThreads, 4) void scan_rows_kernel(
     TileScan<In, Acc> s;
     Acc chunk_total;
     if (tiles == 1) {
-#pragma unroll
-      for (int k = 0; k < kGroups; ++k)
-        load_raw<In, REV, VEC>(xr, D, c0 + lane_off + 256 * k, s.a[k]);
+      load_tile<In, REV, VEC>(xr, D, c0 + lane_off, s.a);
       scan_registers(s);
       if (lane == 0) s_wave[phase][wave] = s.wave_sum;
       __syncthreads();
@@ -289,12 +308,11 @@ __global__ __launch_bounds__(kThreads, 4) void scan_rows_kernel(
       // Pass 1: the chunk total only (the chunk is re-read below, from L2).
       Acc part = (Acc)0;
       for (int tt = 0; tt < tiles; ++tt) {
+        In a[kGroups][4];
+        load_tile<In, REV, VEC>(xr, D, c0 + tt * kTile + lane_off, a);
 #pragma unroll
-        for (int k = 0; k < kGroups; ++k) {
-          In a[4];
-          load_raw<In, REV, VEC>(xr, D, c0 + tt * kTile + lane_off + 256 * k, a);
-          part += (((Acc)a[0] + (Acc)a[1]) + (Acc)a[2]) + (Acc)a[3];
-        }
+        for (int k = 0; k < kGroups; ++k)
+          part += (((Acc)a[k][0] + (Acc)a[k][1]) + (Acc)a[k][2]) + (Acc)a[k][3];
       }
       part = wave_total(part);
       if (lane == 0) s_wave[phase][wave] = part;
@@ -303,30 +321,28 @@ __global__ __launch_bounds__(kThreads, 4) void scan_rows_kernel(
     }
 
     Acc carry = (Acc)0;
+    unsigned prev_done = 0;  // the row's completion count before this chunk's
     if (nchunk > 1) {
       unsigned long long* row_slots = slots + row * nchunk;
       if (wave == 0) {
         if (lane == 0 && chunk + 1 < nchunk)
           __hip_atomic_store(row_slots + chunk, Slot<Acc>::enc(chunk_total), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
-        // The publish must be visible before this chunk counts itself done
-        // (the last counter update zeroes the row's slots): wait for the
-        // store's acknowledgement (vmcnt(0) also counts stores here).
-        __builtin_amdgcn_s_waitcnt(0x0F70);
         const Acc c = carry_in<Acc>(row_slots, chunk, lane, err);
         if (lane == 0) s_carry = c;
-        // Every chunk of the row reads its carry once; the last to do so
-        // zeroes the row's slots (and the counter) for the next call.
-        unsigned prev = 0;
+        // This chunk has read its carry and counts itself done; the last
+        // chunk of the row to do so zeroes the row's slots after its output
+        // (below).  The publish must be visible before the count: wait for
+        // its acknowledgement (vmcnt counts stores in issue order, so for
+        // chunk > 0 the carry loads above already waited for it).  The
+        // count's result is used only by lane 0, after the output stores are
+        // issued (the library is built without the AMDGPU atomic optimizer,
+        // which would broadcast the result to the wave, and wait for it,
+        // right here).
+        __builtin_amdgcn_s_waitcnt(0x0F70);
         if (lane == 0)
-          prev = __hip_atomic_fetch_add(row_done + row, 1u, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT);
-        if (__shfl(prev, 0, 64) == (unsigned)nchunk - 1) {
-          for (int p = lane; p < nchunk - 1; p += 64)
-            __hip_atomic_store(row_slots + p, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          if (lane == 0)
-            __hip_atomic_store(row_done + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+          prev_done = __hip_atomic_fetch_add(row_done + row, 1u, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
       }
       __syncthreads();
       carry = s_carry;
@@ -341,9 +357,7 @@ __global__ __launch_bounds__(kThreads, 4) void scan_rows_kernel(
       Acc run = carry;
       for (int tt = 0; tt < tiles; ++tt) {
         phase ^= 1;
-#pragma unroll
-        for (int k = 0; k < kGroups; ++k)
-          load_raw<In, REV, VEC>(xr, D, c0 + tt * kTile + lane_off + 256 * k, s.a[k]);
+        load_tile<In, REV, VEC>(xr, D, c0 + tt * kTile + lane_off, s.a);
         scan_registers(s);
         if (lane == 0) s_wave[phase][wave] = s.wave_sum;
         __syncthreads();
@@ -352,6 +366,14 @@ __global__ __launch_bounds__(kThreads, 4) void scan_rows_kernel(
         emit_tile<In, Out, Acc, REV, VEC>(s, run + wave_off, yr, D, c0 + tt * kTile + lane_off);
         run += (s_wave[phase][0] + s_wave[phase][1]) + (s_wave[phase][2] + s_wave[phase][3]);
       }
+    }
+    if (nchunk > 1 && wave == 0 && lane == 0 && prev_done == (unsigned)nchunk - 1) {
+      // Every chunk of the row has read its carry: zero the row's slots (and
+      // the counter) for the next call.
+      unsigned long long* row_slots = slots + row * nchunk;
+      for (int p = 0; p < nchunk - 1; ++p)
+        __hip_atomic_store(row_slots + p, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(row_done + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     phase ^= 1;
     // s_carry and the other s_wave buffer are rewritten only after the next

@@ -87,13 +87,16 @@ def layernorm(dev, time_us):
     return out
 
 
-def scan(dev, time_us):
+SCAN_SHAPES = ((64, 65536), (4096, 4096))
+
+
+def scan(dev, time_us, shapes=SCAN_SHAPES):
     import torch
     from framework import capi
     from cases.scan import op
     lib = op._lib()
     out = []
-    for R, D in ((64, 65536), (4096, 4096)):
+    for R, D in shapes:
         g = torch.Generator().manual_seed(0)
         x = (torch.rand(R, D, generator=g) * 2 - 1).to(dev)
         xi = torch.randint(-1000, 1001, (R, D), generator=g, dtype=torch.int32).to(dev)
@@ -157,12 +160,18 @@ def main(argv=None):
     ap.add_argument("--case", default="all", choices=["all", "layernorm", "scan", "spmv"])
     ap.add_argument("--iters", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--scan-shape", default=None, metavar="RxD",
+                    help="time only this scan shape (default: 64x65536 and 4096x4096)")
     ns = ap.parse_args(argv)
     import torch
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     time_us = _timer(dev, ns.iters, ns.warmup)
-    cases = {"layernorm": layernorm, "scan": scan, "spmv": spmv}
+    scan_shapes = SCAN_SHAPES
+    if ns.scan_shape:
+        r, d = (int(v) for v in ns.scan_shape.lower().split("x"))
+        scan_shapes = ((r, d),)
+    cases = {"layernorm": layernorm, "scan": lambda dv, t: scan(dv, t, scan_shapes), "spmv": spmv}
     rows = []
     for name in (cases if ns.case == "all" else [ns.case]):
         for case, what, t, nbytes, detail in cases[name](dev, time_us):

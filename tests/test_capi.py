@@ -37,7 +37,8 @@ def declared_functions(header):
 def _load(modname):
     import importlib
     mod = importlib.import_module(modname)
-    lib = loader.load_library(mod.LIB_NAME, mod.SOURCES, mod.KERNEL_DIR)
+    lib = loader.load_library(mod.LIB_NAME, mod.SOURCES, mod.KERNEL_DIR,
+                              extra_cuda_cflags=getattr(mod, "EXTRA_CUDA_CFLAGS", None))
     return mod.bind_library(lib)
 
 
