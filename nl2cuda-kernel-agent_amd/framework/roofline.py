@@ -1,4 +1,5 @@
-"""Roofline report for the follow-on cases (layernorm, scan, spmv) on one GPU.
+"""Roofline report for the follow-on cases (layernorm, scan, spmv, cosine_sim)
+on one GPU.
 
 For each case's acceptance workload this times every C-ABI entry point
 directly on preallocated device buffers: a 512 MiB read flush before each
@@ -6,11 +7,12 @@ call (so operands come from HBM, not L2 or the MALL), HIP events on the
 launch stream around the call, ``--iters`` timed calls after ``--warmup``.
 Achieved GB/s = algorithmic bytes / mean time (each input read once, each
 output written once; the byte counts are stated per entry), against the
-MI355X HBM peak of 8 TB/s.  Event times include the launch (about 6 us for
-an empty kernel on this box); rocprofv3 kernel times
-(framework/profile.py stats) give the kernel-only figure.
+MI355X HBM peak of 8 TB/s; the MFMA-bound cosine entries also give TFLOP/s
+(2NMD forward, 4NMD backward) against 157.3 TF.  Event times include the
+launch (a few us); rocprofv3 kernel times (framework/profile.py stats) give
+the kernel-only figure.
 
-Usage:  python nl2cuda-kernel-agent_amd/framework/roofline.py [--case all|layernorm|scan|spmv]
+Usage:  python nl2cuda-kernel-agent_amd/framework/roofline.py [--case all|layernorm|scan|spmv|cosine]
 Prints one JSON line per measurement and a closing table.
 """
 
@@ -24,6 +26,7 @@ PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 sys.path.insert(0, PKG)
 
 HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3  # dense fp32 MFMA (AMD published)
 
 
 def _timer(dev, iters, warmup):
@@ -155,9 +158,41 @@ def spmv(dev, time_us):
     return out
 
 
+def cosine(dev, time_us):
+    """Pairwise cosine similarity (fp32 MFMA-bound): flops = 2NMD forward,
+    4NMD backward; bytes = each input read once, each output written once."""
+    import torch
+    from framework import capi
+    from cases.cosine_sim import op
+    lib = op._lib()
+    out = []
+    for n in (2048, 4096):
+        D = 64
+        g = torch.Generator().manual_seed(0)
+        A = torch.randn(n, D, generator=g).to(dev)
+        B = torch.randn(n, D, generator=g).to(dev)
+        dS = torch.randn(n, n, generator=g).to(dev)
+        S = torch.empty(n, n, device=dev)
+        ia, ib = torch.empty(n, device=dev), torch.empty(n, device=dev)
+        dA, dB = torch.empty_like(A), torch.empty_like(B)
+        wsb = lib.cosine_sim_backward_workspace_bytes(n, n, D)
+        ws = torch.empty(max(wsb // 4, 1), device=dev)
+        s, P = capi.stream_of(A), capi.ptr
+        t = time_us(lambda: _check(lib.cosine_sim_forward_f32(P(A), P(B), P(S), P(ia), P(ib), n, n,
+                                                              D, 1e-8, s), lib, "cosine_sim_last_error"))
+        out.append(("cosine_sim", f"forward_f32 [{n},{n}] D=64", t, 4 * n * n + 8 * n * D + 8 * n,
+                    "read A, B; write S, inv_a, inv_b", 2 * n * n * D))
+        t = time_us(lambda: _check(lib.cosine_sim_backward_f32(P(A), P(B), P(ia), P(ib), P(dS), P(dA),
+                                                               P(dB), n, n, D, P(ws), wsb, s),
+                                   lib, "cosine_sim_last_error"))
+        out.append(("cosine_sim", f"backward_f32 [{n},{n}] D=64", t, 4 * n * n + 16 * n * D + 8 * n,
+                    "read dS, A, B, inv_a, inv_b; write dA, dB", 4 * n * n * D))
+    return out
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("--case", default="all", choices=["all", "layernorm", "scan", "spmv"])
+    ap.add_argument("--case", default="all", choices=["all", "layernorm", "scan", "spmv", "cosine"])
     ap.add_argument("--iters", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--scan-shape", default=None, metavar="RxD",
@@ -171,21 +206,27 @@ def main(argv=None):
     if ns.scan_shape:
         r, d = (int(v) for v in ns.scan_shape.lower().split("x"))
         scan_shapes = ((r, d),)
-    cases = {"layernorm": layernorm, "scan": lambda dv, t: scan(dv, t, scan_shapes), "spmv": spmv}
+    cases = {"layernorm": layernorm, "scan": lambda dv, t: scan(dv, t, scan_shapes), "spmv": spmv,
+             "cosine": cosine}
     rows = []
     for name in (cases if ns.case == "all" else [ns.case]):
-        for case, what, t, nbytes, detail in cases[name](dev, time_us):
+        for case, what, t, nbytes, detail, *flops in cases[name](dev, time_us):
             gbs = nbytes / (t * 1e-6) / 1e9
             rec = {"case": case, "entry": what, "us": round(t, 2), "bytes": nbytes,
                    "gbs": round(gbs, 1), "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1),
                    "bytes_are": detail}
+            if flops:
+                tf = flops[0] / (t * 1e-6) / 1e12
+                rec.update(flops=flops[0], tflops=round(tf, 1),
+                           pct_fp32=round(100 * tf / FP32_PEAK_TFLOPS, 1))
             print(json.dumps(rec), flush=True)
             rows.append(rec)
-    print("\n| case | entry | event µs | algorithmic bytes | GB/s | % of 8 TB/s |")
-    print("|---|---|---:|---:|---:|---:|")
+    print("\n| case | entry | event µs | algorithmic bytes | GB/s | % of 8 TB/s | TFLOP/s | % of 157.3 TF |")
+    print("|---|---|---:|---:|---:|---:|---:|---:|")
     for r in rows:
+        tf = f"{r['tflops']:.1f} | {r['pct_fp32']:.1f}" if "tflops" in r else "— | —"
         print(f"| {r['case']} | {r['entry']} | {r['us']:.2f} | {r['bytes']:,} | {r['gbs']:.0f} | "
-              f"{r['pct_hbm']:.1f} |")
+              f"{r['pct_hbm']:.1f} | {tf} |")
     return 0
 
 
