@@ -7,399 +7,26 @@
 // (dx, dgamma, dbeta) from backward (layernorm_forward.cu:302-379,
 // layernorm_backward.cu:176-219).
 //
-// Design (HBM bound: read x, write y; read dy and x, write dx):
-//  * Row-cached path (D % 4 == 0, 16-byte aligned, D <= 8192): TPR threads
-//    own a row (TPR = 64: one wave per row, TPR = 256: one workgroup per
-//    row), each thread keeps V float4 of the row in registers, so the row is
-//    read from HBM exactly once.  Mean and variance are exact two-pass
-//    statistics over the registers; reductions are wave64 butterflies
-//    (DPP / ds_swizzle via __shfl_xor) plus one LDS step across waves.
-//  * Backward: a workgroup walks a contiguous block of rows, prefetching the
-//    next row's dy and x while it finishes the current one, and accumulates
-//    its partial dw / dbias in registers.  The per-block partials ([G][D]
-//    each) are summed by ln_bwd_colsum_kernel in two stream-ordered passes
-//    (column slices x row groups, then the groups' rows), every sum in a
-//    fixed order, so dw and dbias are deterministic.
-//  * Any other shape uses generic kernels that re-read x: one workgroup per
-//    row for y / dx, and ln_bwd_generic_partial_kernel (64 columns x a group
-//    of rows per block) for the partial dw / dbias rows, then the same
-//    column sums.
+// Design: the row-normalisation kernels of csrc/rownorm.h (row-cached
+// two-pass statistics in registers, prefetching backward with per-block
+// dw / dbias partials summed deterministically, generic kernels for other
+// shapes) with the centered, biased policy below.
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
 
 #include "../../../csrc/common.h"
+#include "../../../csrc/rownorm.h"
 #include "layernorm.h"
-
-using nl2k::f32x4;
-using nl2k::load4;
-using nl2k::store4;
-using nl2k::zero4;
 
 namespace {
 
-constexpr int kBlock = 256;
-constexpr int kBwdBlocks = 512;   // level-1 partial rows of dw / dbias
-constexpr int kColsumMaxSplit = 32;   // row groups per column slice in ln_bwd_colsum_kernel
-constexpr int kGenericMaxSplit = 512; // partial rows of the generic path
-
-__device__ __forceinline__ float dot4(f32x4 a, f32x4 b) {
-  return (a[0] * b[0] + a[1] * b[1]) + (a[2] * b[2] + a[3] * b[3]);
-}
-__device__ __forceinline__ float hsum4(f32x4 a) { return (a[0] + a[1]) + (a[2] + a[3]); }
-
-// Sum over the TPR threads that share a row (TPR = 64 or 256), result in all
-// of them.  `red` is a per-block LDS scratch of at least 2 * 4 floats.
-template <int TPR>
-__device__ __forceinline__ void row_sum2(float& a, float& b, float* red) {
-  a = nl2k::wave_sum(a);
-  b = nl2k::wave_sum(b);
-  if (TPR == 256) {
-    const int wave = threadIdx.x >> 6;
-    __syncthreads();  // red may still be read from the previous use
-    if ((threadIdx.x & 63) == 0) {
-      red[wave] = a;
-      red[4 + wave] = b;
-    }
-    __syncthreads();
-    a = (red[0] + red[1]) + (red[2] + red[3]);
-    b = (red[4] + red[5]) + (red[6] + red[7]);
-  }
-}
-
-template <int TPR>
-__device__ __forceinline__ float row_sum1(float a, float* red) {
-  float b = 0.f;
-  row_sum2<TPR>(a, b, red);
-  return a;
-}
-
-// ------------------------------------------------------------------ forward
-// FULL: D/4 == V * TPR, so every thread's V float4 are in range and the
-// loads need no guard (guards become branches that defeat load batching).
-template <int TPR, int V, bool FULL>
-__global__ __launch_bounds__(kBlock) void ln_fwd_kernel(
-    const float* __restrict__ x, const float* __restrict__ w,
-    const float* __restrict__ bias, float* __restrict__ y,
-    float* __restrict__ mean_out, float* __restrict__ rstd_out, int64_t B,
-    int D, float eps) {
-  __shared__ float red[8];
-  constexpr int RPB = kBlock / TPR;
-  const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;
-  const int t = threadIdx.x % TPR;
-  const int D4 = D >> 2;
-  const bool live = row < B;  // uniform per row group (and per block for TPR = 256)
-  const f32x4* xr = reinterpret_cast<const f32x4*>(x + (live ? row : 0) * D);
-
-  f32x4 v[V];
-  float s = 0.f;
-#pragma unroll
-  for (int k = 0; k < V; ++k) {
-    const int c = t + k * TPR;
-    if (FULL) {
-      v[k] = xr[c];
-    } else {
-      const f32x4 val = xr[min(c, D4 - 1)];
-      v[k] = (live && c < D4) ? val : zero4();
-    }
-    s += hsum4(v[k]);
-  }
-  const float inv_d = 1.f / (float)D;
-  const float mu = row_sum1<TPR>(s, red) * inv_d;
-  float q = 0.f;
-#pragma unroll
-  for (int k = 0; k < V; ++k) {
-    const int c = t + k * TPR;
-    if (FULL || c < D4) {
-      const f32x4 dv = v[k] - mu;
-      q += dot4(dv, dv);
-    }
-  }
-  const float var = row_sum1<TPR>(q, red) * inv_d;
-  const float rs = 1.f / sqrtf(var + eps);
-  if (!live) return;
-  if (t == 0) {
-    mean_out[row] = mu;
-    rstd_out[row] = rs;
-  }
-  const f32x4* w4 = reinterpret_cast<const f32x4*>(w);
-  const f32x4* b4 = reinterpret_cast<const f32x4*>(bias);
-  f32x4* yr = reinterpret_cast<f32x4*>(y + row * D);
-#pragma unroll
-  for (int k = 0; k < V; ++k) {
-    const int c = t + k * TPR;
-    if (FULL || c < D4) yr[c] = (v[k] - mu) * rs * w4[c] + b4[c];
-  }
-}
-
-// Generic forward: one workgroup per row, any D and alignment.
-__global__ __launch_bounds__(kBlock) void ln_fwd_generic_kernel(
-    const float* __restrict__ x, const float* __restrict__ w,
-    const float* __restrict__ bias, float* __restrict__ y,
-    float* __restrict__ mean_out, float* __restrict__ rstd_out, int64_t D,
-    float eps) {
-  __shared__ float red[8];
-  const int64_t row = blockIdx.x;
-  const float* xr = x + row * D;
-  float s = 0.f;
-  for (int64_t c = threadIdx.x; c < D; c += kBlock) s += xr[c];
-  const float mu = row_sum1<kBlock>(s, red) / (float)D;
-  float q = 0.f;
-  for (int64_t c = threadIdx.x; c < D; c += kBlock) {
-    const float d = xr[c] - mu;
-    q = fmaf(d, d, q);
-  }
-  const float rs = 1.f / sqrtf(row_sum1<kBlock>(q, red) / (float)D + eps);
-  if (threadIdx.x == 0) {
-    mean_out[row] = mu;
-    rstd_out[row] = rs;
-  }
-  for (int64_t c = threadIdx.x; c < D; c += kBlock)
-    y[row * D + c] = (xr[c] - mu) * rs * w[c] + bias[c];
-}
-
-// ----------------------------------------------------------------- backward
-// Level 1: block b handles rows [b*rpb, min(B, (b+1)*rpb)), one row at a
-// time with all 256 threads (V float4 per thread), and writes its partial
-// dw / dbias row to pw[b], pb[b].
-template <int V, bool FULL>
-__global__ __launch_bounds__(kBlock) void ln_bwd_kernel(
-    const float* __restrict__ dy, const float* __restrict__ x,
-    const float* __restrict__ w, const float* __restrict__ mean,
-    const float* __restrict__ rstd, float* __restrict__ dx,
-    float* __restrict__ pw, float* __restrict__ pb, int64_t B, int D,
-    int64_t rpb) {
-  __shared__ float red[8];
-  const int t = threadIdx.x;
-  const int D4 = D >> 2;
-  const int64_t r0 = (int64_t)blockIdx.x * rpb;
-  const int64_t r1 = min(B, r0 + rpb);
-  const f32x4* w4 = reinterpret_cast<const f32x4*>(w);
-
-  f32x4 wv[V], aw[V], ab[V], gcur[V], xcur[V], gnext[V], xnext[V];
-#pragma unroll
-  for (int k = 0; k < V; ++k) {
-    const int c = t + k * kBlock;
-    const f32x4 wk = w4[FULL ? c : min(c, D4 - 1)];
-    wv[k] = (FULL || c < D4) ? wk : zero4();
-    aw[k] = zero4();
-    ab[k] = zero4();
-  }
-  auto load_row = [&](int64_t r, f32x4 (&g)[V], f32x4 (&xv)[V]) {
-    const f32x4* dyr = reinterpret_cast<const f32x4*>(dy + r * D);
-    const f32x4* xr = reinterpret_cast<const f32x4*>(x + r * D);
-#pragma unroll
-    for (int k = 0; k < V; ++k) {
-      const int c = t + k * kBlock;
-      if (FULL) {
-        g[k] = dyr[c];
-        xv[k] = xr[c];
-      } else {
-        const int cc = min(c, D4 - 1);
-        const f32x4 a = dyr[cc], b = xr[cc];
-        g[k] = c < D4 ? a : zero4();
-        xv[k] = c < D4 ? b : zero4();
-      }
-    }
-  };
-  if (r0 < r1) load_row(r0, gcur, xcur);
-  const float inv_d = 1.f / (float)D;
-  for (int64_t r = r0; r < r1; ++r) {
-    // Unconditional prefetch (the last row re-reads itself): a conditional
-    // one makes the number of loads in flight path dependent and the
-    // compiler then waits for all of them before using the current row.
-    load_row(min(r + 1, r1 - 1), gnext, xnext);
-    const float mu = mean[r], rs = rstd[r];
-    float sg = 0.f, sgx = 0.f;
-    f32x4 xh[V];
-#pragma unroll
-    for (int k = 0; k < V; ++k) {
-      xh[k] = (xcur[k] - mu) * rs;
-      const f32x4 g = gcur[k] * wv[k];
-      sg += hsum4(g);
-      sgx += dot4(g, xh[k]);
-      aw[k] += gcur[k] * xh[k];
-      ab[k] += gcur[k];
-    }
-    row_sum2<kBlock>(sg, sgx, red);
-    const float mg = sg * inv_d, mgx = sgx * inv_d;
-    f32x4* dxr = reinterpret_cast<f32x4*>(dx + r * D);
-#pragma unroll
-    for (int k = 0; k < V; ++k) {
-      const int c = t + k * kBlock;
-      if (FULL || c < D4) dxr[c] = rs * (gcur[k] * wv[k] - mg - xh[k] * mgx);
-    }
-#pragma unroll
-    for (int k = 0; k < V; ++k) {
-      gcur[k] = gnext[k];
-      xcur[k] = xnext[k];
-    }
-  }
-  f32x4* pw4 = reinterpret_cast<f32x4*>(pw + (int64_t)blockIdx.x * D);
-  f32x4* pb4 = reinterpret_cast<f32x4*>(pb + (int64_t)blockIdx.x * D);
-#pragma unroll
-  for (int k = 0; k < V; ++k) {
-    const int c = t + k * kBlock;
-    if (FULL || c < D4) {
-      pw4[c] = aw[k];
-      pb4[c] = ab[k];
-    }
-  }
-}
-
-// Generic backward (any D / alignment): one workgroup per row writes dx;
-// ln_bwd_generic_param_kernel then sums dw / dbias column by column.
-__global__ __launch_bounds__(kBlock) void ln_bwd_generic_kernel(
-    const float* __restrict__ dy, const float* __restrict__ x,
-    const float* __restrict__ w, const float* __restrict__ mean,
-    const float* __restrict__ rstd, float* __restrict__ dx, int64_t D) {
-  __shared__ float red[8];
-  const int64_t row = blockIdx.x;
-  const float mu = mean[row], rs = rstd[row];
-  float sg = 0.f, sgx = 0.f;
-  for (int64_t c = threadIdx.x; c < D; c += kBlock) {
-    const float xh = (x[row * D + c] - mu) * rs;
-    const float g = dy[row * D + c] * w[c];
-    sg += g;
-    sgx = fmaf(g, xh, sgx);
-  }
-  row_sum2<kBlock>(sg, sgx, red);
-  const float mg = sg / (float)D, mgx = sgx / (float)D;
-  for (int64_t c = threadIdx.x; c < D; c += kBlock) {
-    const float xh = (x[row * D + c] - mu) * rs;
-    dx[row * D + c] = rs * (dy[row * D + c] * w[c] - mg - xh * mgx);
-  }
-}
-
-// Partial dw / dbias rows for the generic path.  Block (cs, g) covers the
-// 64 columns [64 cs, 64 cs + 64) and rows [g per, min(B, (g + 1) per)); wave
-// w takes rows a + w, a + w + 4, ... and the four waves combine in LDS, in a
-// fixed order, into pw[g], pb[g].
-__global__ __launch_bounds__(kBlock) void ln_bwd_generic_partial_kernel(
-    const float* __restrict__ dy, const float* __restrict__ x,
-    const float* __restrict__ mean, const float* __restrict__ rstd, int64_t B,
-    int64_t D, int64_t per, float* __restrict__ pw, float* __restrict__ pb) {
-  __shared__ float sw[4][64], sb[4][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t c = (int64_t)blockIdx.x * 64 + lane;
-  const int64_t cc = min(c, D - 1);
-  const int64_t a = (int64_t)blockIdx.y * per, e = min(B, a + per);
-  float aw = 0.f, ab = 0.f;
-#pragma unroll 4
-  for (int64_t r = a + wave; r < e; r += 4) {
-    const float g = dy[r * D + cc];
-    aw = fmaf(g, (x[r * D + cc] - mean[r]) * rstd[r], aw);
-    ab += g;
-  }
-  sw[wave][lane] = aw;
-  sb[wave][lane] = ab;
-  __syncthreads();
-  if (wave == 0 && c < D) {
-    pw[blockIdx.y * D + c] = (sw[0][lane] + sw[1][lane]) + (sw[2][lane] + sw[3][lane]);
-    pb[blockIdx.y * D + c] = (sb[0][lane] + sb[1][lane]) + (sb[2][lane] + sb[3][lane]);
-  }
-}
-
-// Column sums of partial rows, deterministic: block (cs, g) covers 64
-// column units (T = float4: four columns per unit, T = float: one) of slice
-// cs and rows [g per, min(R, (g + 1) per)) of in_w / in_b ([R][D]); wave w
-// takes rows a + w, a + w + 4, ... and the four waves combine in LDS, in a
-// fixed order, into row g of out_w / out_b.  Launched once with gridDim.y =
-// 1 (out = dw, dbias) or twice, the second pass summing the first's rows.
-// Stream order makes the first pass's rows visible to the second; a
-// last-block-finishes scheme would need a device-scope fence per block,
-// i.e. an L2 write-back per block on this multi-XCD part.
-template <typename T>
-__global__ __launch_bounds__(kBlock) void ln_bwd_colsum_kernel(
-    const float* __restrict__ in_w, const float* __restrict__ in_b, int64_t R,
-    int64_t D, int64_t per, float* __restrict__ out_w, float* __restrict__ out_b) {
-  constexpr int VC = sizeof(T) / sizeof(float);
-  __shared__ T sw[4][64], sb[4][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t DU = D / VC;
-  const int64_t cu = (int64_t)blockIdx.x * 64 + lane;
-  const int64_t cc = min(cu, DU - 1);
-  const T* iw = reinterpret_cast<const T*>(in_w);
-  const T* ib = reinterpret_cast<const T*>(in_b);
-  const int64_t a = (int64_t)blockIdx.y * per, e = min(R, a + per);
-  T aw = (T)0.f, ab = (T)0.f;
-#pragma unroll 4
-  for (int64_t r = a + wave; r < e; r += 4) {
-    aw += iw[r * DU + cc];
-    ab += ib[r * DU + cc];
-  }
-  sw[wave][lane] = aw;
-  sb[wave][lane] = ab;
-  __syncthreads();
-  if (wave == 0 && cu < DU) {
-    reinterpret_cast<T*>(out_w)[blockIdx.y * DU + cu] =
-        (sw[0][lane] + sw[1][lane]) + (sw[2][lane] + sw[3][lane]);
-    reinterpret_cast<T*>(out_b)[blockIdx.y * DU + cu] =
-        (sb[0][lane] + sb[1][lane]) + (sb[2][lane] + sb[3][lane]);
-  }
-}
-
-__global__ __launch_bounds__(kBlock) void ln_fill_zero_kernel(float* __restrict__ a,
-                                                             float* __restrict__ b,
-                                                             int64_t n) {
-  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * kBlock) {
-    a[i] = 0.f;
-    b[i] = 0.f;
-  }
-}
-
-// ----------------------------------------------------------------- planning
-struct Plan {
-  bool cached = false;  // row-cached vector path
-  int tpr = 256;        // forward threads per row
-  int v = 4;            // float4 per thread
-  int64_t G = 0;        // partial rows of dw / dbias
-  int64_t rpb = 0;      // rows per block: backward blocks (cached) or partial groups (generic)
-  int64_t S = 0;        // row groups per column slice in ln_bwd_colsum_kernel
-  int64_t cper = 0;     // partial rows per such group
+// mean-subtracted statistics over D, a bias, stat0 = mean, stat1 = rstd.
+struct LayerNormRows {
+  static constexpr bool kCentered = true, kBias = true;
+  __device__ static float stat1(float rs, float) { return rs; }
+  __device__ static float rs(float stat1) { return stat1; }
 };
-
-Plan plan(int64_t B, int64_t D, bool aligned) {
-  Plan p;
-  p.cached = aligned && D % 4 == 0 && D <= 8192;
-  if (p.cached) {
-    const int64_t d4 = D / 4;
-    if (d4 <= 64) {
-      p.tpr = 64;
-      p.v = 1;
-    } else if (d4 <= 256) {
-      p.tpr = 64;
-      p.v = 4;
-    } else {
-      p.tpr = 256;
-      p.v = d4 <= 512 ? 2 : d4 <= 1024 ? 4 : 8;
-    }
-    p.rpb = std::max<int64_t>(1, nl2k::ceil_div(B, kBwdBlocks));
-  } else {
-    // ~2048 blocks of 64 columns x (B / S1) rows
-    const int64_t slices = nl2k::ceil_div(D, 64);
-    const int64_t s1 = std::min<int64_t>(
-        std::min<int64_t>(std::max<int64_t>(1, nl2k::ceil_div(2048, slices)), kGenericMaxSplit),
-        std::max<int64_t>(B, 1));
-    p.rpb = std::max<int64_t>(1, nl2k::ceil_div(B, s1));
-  }
-  p.G = B > 0 ? nl2k::ceil_div(B, p.rpb) : 0;
-  // column sums: ~512 blocks of 256 columns (float4) x (G / S) partial rows
-  const int64_t slices4 = nl2k::ceil_div(D, 256);
-  const int64_t s2 = std::min<int64_t>(
-      std::min<int64_t>(std::max<int64_t>(1, nl2k::ceil_div(512, slices4)), kColsumMaxSplit),
-      std::max<int64_t>(p.G, 1));
-  p.cper = std::max<int64_t>(1, nl2k::ceil_div(p.G, s2));
-  p.S = p.G > 0 ? nl2k::ceil_div(p.G, p.cper) : 0;
-  return p;
-}
-
-// Workspace: partial rows (2 G D) and, when the column sums take two
-// passes, the first pass's rows (2 S D).
-size_t workspace_floats(int64_t D, const Plan& p) {
-  return (size_t)(2 * p.G * D + (p.S > 1 ? 2 * p.S * D : 0));
-}
 
 int validate(int64_t B, int64_t D, const char* who) {
   if (B < 0 || D < 1)
@@ -427,40 +54,13 @@ int layernorm_forward_f32(const float* x, const float* w, const float* bias,
   if (B == 0) return nl2k::succeed();
   if (!x || !w || !bias || !y || !mean || !rstd)
     return nl2k::fail(NL2K_ERR_NULL, "layernorm_forward_f32: null pointer argument");
-  const bool aligned = nl2k::aligned16(x) && nl2k::aligned16(w) &&
-                       nl2k::aligned16(bias) && nl2k::aligned16(y);
-  const Plan p = plan(B, D, aligned);
-  if (p.cached) {
-    const int rpb = kBlock / p.tpr;
-    const dim3 grid((unsigned)nl2k::ceil_div(B, rpb));
-#define LN_FWD(TPR, V)                                                                    \
-  do {                                                                                     \
-    if (D / 4 == (TPR) * (V))                                                              \
-      hipLaunchKernelGGL((ln_fwd_kernel<TPR, V, true>), grid, dim3(kBlock), 0, stream, x, w, \
-                         bias, y, mean, rstd, B, (int)D, eps);                             \
-    else                                                                                   \
-      hipLaunchKernelGGL((ln_fwd_kernel<TPR, V, false>), grid, dim3(kBlock), 0, stream, x, \
-                         w, bias, y, mean, rstd, B, (int)D, eps);                          \
-  } while (0)
-    if (p.tpr == 64 && p.v == 1) LN_FWD(64, 1);
-    else if (p.tpr == 64) LN_FWD(64, 4);
-    else if (p.v == 2) LN_FWD(256, 2);
-    else if (p.v == 4) LN_FWD(256, 4);
-    else LN_FWD(256, 8);
-#undef LN_FWD
-    return nl2k::check_launch("layernorm_forward_f32");
-  }
-  hipLaunchKernelGGL(ln_fwd_generic_kernel, dim3((unsigned)B), dim3(kBlock), 0, stream, x, w,
-                     bias, y, mean, rstd, D, eps);
-  return nl2k::check_launch("layernorm_forward_f32 (generic)");
+  return nl2k::rownorm::run_forward<LayerNormRows>(x, w, bias, y, mean, rstd, B, D, eps, stream,
+                                                   "layernorm_forward_f32");
 }
 
 size_t layernorm_backward_workspace_bytes(int64_t B, int64_t D) {
   if (validate(B, D, "layernorm_backward_workspace_bytes")) return 0;
-  // Pointer alignment picks the path at call time: cover both.
-  const size_t cached = workspace_floats(D, plan(B, D, true));
-  const size_t generic = workspace_floats(D, plan(B, D, false));
-  return std::max(cached, generic) * sizeof(float);
+  return nl2k::rownorm::backward_workspace_bytes<LayerNormRows>(B, D);
 }
 
 int layernorm_backward_f32(const float* dy, const float* x, const float* w,
@@ -468,78 +68,25 @@ int layernorm_backward_f32(const float* dy, const float* x, const float* w,
                            float* dw, float* dbias, int64_t B, int64_t D,
                            void* workspace, size_t workspace_bytes,
                            hipStream_t stream) {
-  int st = validate(B, D, "layernorm_backward_f32");
+  const char* who = "layernorm_backward_f32";
+  int st = validate(B, D, who);
   if (st) return st;
   if (!dw || !dbias || (B > 0 && (!dy || !x || !w || !mean || !rstd || !dx)))
     return nl2k::fail(NL2K_ERR_NULL, "layernorm_backward_f32: null pointer argument");
-  if (B == 0) {  // empty batch: the parameter gradients are zero
-    hipLaunchKernelGGL(ln_fill_zero_kernel, dim3((unsigned)std::min<int64_t>(nl2k::ceil_div(D, kBlock), 1024)),
-                       dim3(kBlock), 0, stream, dw, dbias, D);
-    return nl2k::check_launch("layernorm_backward_f32 (zero)");
-  }
+  if (B == 0)  // empty batch: the parameter gradients are zero
+    return nl2k::rownorm::fill_zero(dw, dbias, D, stream, "layernorm_backward_f32 (zero)");
   const bool aligned = nl2k::aligned16(dy) && nl2k::aligned16(x) && nl2k::aligned16(w) &&
                        nl2k::aligned16(dx);
-  const Plan p = plan(B, D, aligned);
-  const size_t need = workspace_floats(D, p) * sizeof(float);
+  const size_t need = nl2k::rownorm::workspace_floats<LayerNormRows>(
+                          D, nl2k::rownorm::plan(B, D, aligned)) * sizeof(float);
   if (!workspace || workspace_bytes < need)
     return nl2k::fail(NL2K_ERR_WORKSPACE,
                       "layernorm_backward_f32: workspace of %zu bytes required, got %zu", need,
                       workspace ? workspace_bytes : (size_t)0);
   if (!nl2k::aligned16(workspace))
     return nl2k::fail(NL2K_ERR_ALIGN, "layernorm_backward_f32: workspace must be 16-byte aligned");
-  float* ws = static_cast<float*>(workspace);
-  float* pw = ws;
-  float* pb = pw + p.G * D;
-  float* l2w = pb + p.G * D;
-  float* l2b = l2w + p.S * D;
-  if (p.cached) {
-#define LN_BWD(V)                                                                          \
-  do {                                                                                     \
-    if (D / 4 == 256 * (V))                                                                \
-      hipLaunchKernelGGL((ln_bwd_kernel<V, true>), dim3((unsigned)p.G), dim3(kBlock), 0,   \
-                         stream, dy, x, w, mean, rstd, dx, pw, pb, B, (int)D, p.rpb);      \
-    else                                                                                   \
-      hipLaunchKernelGGL((ln_bwd_kernel<V, false>), dim3((unsigned)p.G), dim3(kBlock), 0,  \
-                         stream, dy, x, w, mean, rstd, dx, pw, pb, B, (int)D, p.rpb);      \
-  } while (0)
-    const int64_t d4 = D / 4;
-    if (d4 <= 256) LN_BWD(1);
-    else if (d4 <= 512) LN_BWD(2);
-    else if (d4 <= 1024) LN_BWD(4);
-    else LN_BWD(8);
-#undef LN_BWD
-    st = nl2k::check_launch("layernorm_backward_f32");
-  } else {
-    hipLaunchKernelGGL(ln_bwd_generic_kernel, dim3((unsigned)B), dim3(kBlock), 0, stream, dy, x,
-                       w, mean, rstd, dx, D);
-    st = nl2k::check_launch("layernorm_backward_f32 (generic)");
-    if (st) return st;
-    hipLaunchKernelGGL(ln_bwd_generic_partial_kernel,
-                       dim3((unsigned)nl2k::ceil_div(D, 64), (unsigned)p.G), dim3(kBlock), 0,
-                       stream, dy, x, mean, rstd, B, D, p.rpb, pw, pb);
-    st = nl2k::check_launch("layernorm_backward_f32 (generic partials)");
-  }
-  if (st) return st;
-  const bool vec = D % 4 == 0 && nl2k::aligned16(dw) && nl2k::aligned16(dbias);
-  const unsigned slices = (unsigned)nl2k::ceil_div(D, vec ? 256 : 64);
-  auto colsum = [&](const float* iw, const float* ib, int64_t R, int64_t per, unsigned groups,
-                    float* ow, float* ob) {
-    if (vec)
-      hipLaunchKernelGGL(ln_bwd_colsum_kernel<f32x4>, dim3(slices, groups), dim3(kBlock), 0,
-                         stream, iw, ib, R, D, per, ow, ob);
-    else
-      hipLaunchKernelGGL(ln_bwd_colsum_kernel<float>, dim3(slices, groups), dim3(kBlock), 0,
-                         stream, iw, ib, R, D, per, ow, ob);
-  };
-  if (p.S > 1) {
-    colsum(pw, pb, p.G, p.cper, (unsigned)p.S, l2w, l2b);
-    st = nl2k::check_launch("layernorm_backward_f32 (column sums)");
-    if (st) return st;
-    colsum(l2w, l2b, p.S, p.S, 1u, dw, dbias);
-  } else {
-    colsum(pw, pb, p.G, p.G, 1u, dw, dbias);
-  }
-  return nl2k::check_launch("layernorm_backward_f32 (column sums)");
+  return nl2k::rownorm::run_backward<LayerNormRows>(dy, x, w, mean, rstd, dx, dw, dbias, B, D,
+                                                    static_cast<float*>(workspace), stream, who);
 }
 
 }  // extern "C"

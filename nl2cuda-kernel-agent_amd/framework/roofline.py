@@ -1,5 +1,5 @@
-"""Roofline report for the follow-on cases (layernorm, scan, spmv, cosine_sim)
-on one GPU.
+"""Roofline report for the follow-on cases (layernorm, l2norm_scale, scan,
+spmv, cosine_sim) on one GPU.
 
 For each case's acceptance workload this times every C-ABI entry point
 directly on preallocated device buffers: a 512 MiB read flush before each
@@ -12,7 +12,8 @@ MI355X HBM peak of 8 TB/s; the MFMA-bound cosine entries also give TFLOP/s
 launch (a few us); rocprofv3 kernel times (framework/profile.py stats) give
 the kernel-only figure.
 
-Usage:  python nl2cuda-kernel-agent_amd/framework/roofline.py [--case all|layernorm|scan|spmv|cosine]
+Usage:  python nl2cuda-kernel-agent_amd/framework/roofline.py
+            [--case all|layernorm|l2norm|scan|spmv|cosine]
 Prints one JSON line per measurement and a closing table.
 """
 
@@ -91,6 +92,36 @@ def layernorm(dev, time_us):
 
 
 SCAN_SHAPES = ((64, 65536), (4096, 4096))
+
+
+def l2norm(dev, time_us):
+    """L2-norm-scale (HBM-bound): forward reads X and g, writes Y and the
+    norms; backward reads dY, X, g and the norms, writes dX and dg."""
+    import torch
+    from framework import capi
+    from cases.l2norm_scale import op, config
+    lib = op._lib()
+    out = []
+    for N, D in config.BENCH_SHAPES:
+        gen = torch.Generator().manual_seed(0)
+        x = torch.randn(N, D, generator=gen).to(dev)
+        g = torch.randn(D, generator=gen).to(dev)
+        dy = torch.randn(N, D, generator=gen).to(dev)
+        y, dx = torch.empty_like(x), torch.empty_like(x)
+        norm, dg = torch.empty(N, device=dev), torch.empty(D, device=dev)
+        wsb = lib.l2norm_scale_backward_workspace_bytes(N, D)
+        ws = torch.empty(max(wsb // 4, 1), device=dev)
+        s, P = capi.stream_of(x), capi.ptr
+        t = time_us(lambda: _check(lib.l2norm_scale_forward_f32(P(x), P(g), P(y), P(norm), N, D,
+                                                                1e-6, s), lib, "l2norm_scale_last_error"))
+        out.append(("l2norm_scale", f"forward_f32 [{N},{D}]", t, 8 * N * D + 4 * D + 4 * N,
+                    "read X, g; write Y, norm"))
+        t = time_us(lambda: _check(lib.l2norm_scale_backward_f32(P(dy), P(x), P(g), P(norm), P(dx),
+                                                                 P(dg), N, D, P(ws), wsb, s),
+                                   lib, "l2norm_scale_last_error"))
+        out.append(("l2norm_scale", f"backward_f32 [{N},{D}]", t, 12 * N * D + 8 * D + 4 * N,
+                    "read dY, X, g, norm; write dX, dg"))
+    return out
 
 
 def scan(dev, time_us, shapes=SCAN_SHAPES):
@@ -192,7 +223,8 @@ def cosine(dev, time_us):
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("--case", default="all", choices=["all", "layernorm", "scan", "spmv", "cosine"])
+    ap.add_argument("--case", default="all",
+                    choices=["all", "layernorm", "l2norm", "scan", "spmv", "cosine"])
     ap.add_argument("--iters", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--scan-shape", default=None, metavar="RxD",
@@ -206,8 +238,8 @@ def main(argv=None):
     if ns.scan_shape:
         r, d = (int(v) for v in ns.scan_shape.lower().split("x"))
         scan_shapes = ((r, d),)
-    cases = {"layernorm": layernorm, "scan": lambda dv, t: scan(dv, t, scan_shapes), "spmv": spmv,
-             "cosine": cosine}
+    cases = {"layernorm": layernorm, "l2norm": l2norm,
+             "scan": lambda dv, t: scan(dv, t, scan_shapes), "spmv": spmv, "cosine": cosine}
     rows = []
     for name in (cases if ns.case == "all" else [ns.case]):
         for case, what, t, nbytes, detail, *flops in cases[name](dev, time_us):

@@ -18,7 +18,7 @@ INCLUDE = os.path.join(REPO, "include")
 # header -> op module that loads the library implementing it
 HEADERS = {"rbf.h": "cases.rbf.op", "layernorm.h": "cases.layernorm.op",
            "scan.h": "cases.scan.op", "spmv.h": "cases.spmv.op",
-           "cosine_sim.h": "cases.cosine_sim.op"}
+           "cosine_sim.h": "cases.cosine_sim.op", "l2norm_scale.h": "cases.l2norm_scale.op"}
 
 STATUS = {}
 with open(os.path.join(INCLUDE, "nl2k_status.h")) as _f:
@@ -179,6 +179,25 @@ def test_cosine_sim_argument_validation_without_gpu():
     need = lib.cosine_sim_backward_workspace_bytes(64, 64, 64)
     st = lib.cosine_sim_backward_f32(fake, fake, fake, fake, fake, fake, fake, 64, 64, 64, fake,
                                      need - 4, None)
+    assert st == STATUS["NL2K_ERR_WORKSPACE"]
+
+
+def test_l2norm_scale_argument_validation_without_gpu():
+    lib = _load("cases.l2norm_scale.op")
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: every call below fails validation
+    st = lib.l2norm_scale_forward_f32(fake, fake, fake, fake, -1, 64, 1e-6, None)
+    assert st == STATUS["NL2K_ERR_SHAPE"]
+    st = lib.l2norm_scale_forward_f32(fake, fake, fake, fake, 4, 64, float("nan"), None)
+    assert st == STATUS["NL2K_ERR_VALUE"]
+    st = lib.l2norm_scale_forward_f32(fake, None, fake, fake, 4, 64, 1e-6, None)
+    assert st == STATUS["NL2K_ERR_NULL"]
+    # one partial dg row per backward block (512 blocks at 16384 rows) plus the
+    # first column-sum pass's rows; no bias rows
+    need = lib.l2norm_scale_backward_workspace_bytes(16384, 1024)
+    ln = _load("cases.layernorm.op")
+    assert 2 * need == ln.layernorm_backward_workspace_bytes(16384, 1024)
+    st = lib.l2norm_scale_backward_f32(fake, fake, fake, fake, fake, fake, 16384, 1024, fake,
+                                       need - 4, None)
     assert st == STATUS["NL2K_ERR_WORKSPACE"]
 
 
