@@ -1,7 +1,7 @@
 /*
  * Status codes shared by every C-ABI library of this package
  * (librbf_hip.so, liblayernorm_hip.so, libscan_hip.so, libspmv_hip.so,
- * libcosine_sim_hip.so, libl2norm_scale_hip.so).
+ * libcosine_sim_hip.so, libl2norm_scale_hip.so, libsoftmax_ce_hip.so).
  *
  * Every entry point returns 0 on success or one of the negative codes below.
  * Argument validation runs before any HIP call, so a rejected call never

@@ -1,0 +1,453 @@
+// Softmax cross-entropy loss, forward and backward, fp32 logits and int64
+// labels, for MI355X (gfx950).  C-ABI in include/softmax_ce.h.
+//
+// Reference semantics (cases/softmax_ce/reference.py:15-21):
+//   lse[b]  = logsumexp_c logits[b, c]
+//   loss    = mean_b (lse[b] - logits[b, labels[b]])
+// and by autograd, for the upstream scalar gradient gout,
+//   dlogits[b, c] = gout / B * (exp(logits[b, c] - lse[b]) - [c == labels[b]])
+// (the reference kernels recompute the row max and sum in the backward and
+// accumulate the loss with one atomicAdd per row,
+// softmax_ce_forward.cu:14-50, softmax_ce_backward.cu:13-56).
+//
+// Design (HBM bound):
+//  * Forward: TPR threads own a row (TPR = 64 up to C = 1024, else 256) and
+//    keep its V float4 in registers, so the row is read once; every thread
+//    issues the loads of R rows before using any.  The row max, then sum
+//    exp2((x - max) log2 e), reduced with DPP lane moves (plus one LDS step
+//    for TPR = 256); the label's logit is loaded directly.  At most 1024
+//    workgroups stride over the rows; each writes lse per row and one partial
+//    loss sum, and a one-workgroup finalize kernel adds the partials in a
+//    fixed order, so the loss is deterministic (a last-workgroup reduction
+//    through agent-scope slots in the same launch measured slower: its
+//    serial slot round trips outlast the second launch).
+//  * Backward: lse saved by the forward turns the gradient into a pure
+//    streaming pass (read logits, write dlogits, no reductions), laid out
+//    like the forward so each row's lse and label are read once.
+//  * A label outside [0, C) makes its row's loss term and gradient NaN (the
+//    reference would index out of the row; torch raises).
+//  * C not a multiple of 4, misaligned rows or C > 8192 use a generic
+//    workgroup-per-row kernel (three passes over the row from L2).
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+
+#include "../../../csrc/common.h"
+#include "softmax_ce.h"
+
+using nl2k::f32x4;
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr int kFwdBlocks = 1024;  // most forward workgroups (one partial loss each)
+static_assert(kFwdBlocks % 256 == 0, "the finalize kernel reads kFwdBlocks / 256 per thread");
+// Workspace of the forward: one partial loss per workgroup.
+constexpr size_t kWorkspaceBytes = sizeof(float) * (size_t)kFwdBlocks;
+
+// Reduce N values per thread over the TPR threads that share a row (TPR = 64:
+// one wave; TPR = 256: the workgroup, through `red`, >= 4 * N floats); the
+// results land in every thread.  MAX selects fmaxf, else +.
+template <int TPR, int N, bool MAX>
+__device__ __forceinline__ void row_reduce(float (&a)[N], float* red) {
+#pragma unroll
+  for (int j = 0; j < N; ++j) a[j] = MAX ? nl2k::wave_max_dpp(a[j]) : nl2k::wave_sum_dpp(a[j]);
+  if (TPR == 256) {
+    const int wave = threadIdx.x >> 6;
+    __syncthreads();  // red may still be read from the previous use
+    if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+      for (int j = 0; j < N; ++j) red[4 * j + wave] = a[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const float* q = red + 4 * j;
+      a[j] = MAX ? fmaxf(fmaxf(q[0], q[1]), fmaxf(q[2], q[3])) : (q[0] + q[1]) + (q[2] + q[3]);
+    }
+  }
+}
+
+// Column of the row's label, or -1 when the label is outside [0, C).
+__device__ __forceinline__ int label_col(int64_t lab, int64_t C) {
+  return (lab >= 0 && lab < C) ? (int)lab : -1;
+}
+
+// Rows per block step for a width class: enough rows that each thread has
+// about eight float4 loads in flight before the first is used.
+template <int V>
+constexpr int rows_in_flight() {
+  return V == 1 ? 8 : V == 2 ? 4 : 2;
+}
+
+// Row-cached forward.  TPR threads own a row and keep its V float4 per
+// thread in registers; a block step covers R row groups of kBlock / TPR rows
+// (all R rows' loads issued before any is used), block steps are strided by
+// the grid.  Rows past B are clamped to B - 1 for the loads and discarded.
+// Thread 0 of each row group keeps its rows' loss terms in row order; the
+// workgroup's sum (groups added in a fixed order) goes to
+// partial[blockIdx.x].
+template <int TPR, int V, bool FULL>
+__global__ __launch_bounds__(kBlock) void sce_fwd_kernel(
+    const float* __restrict__ logits, const int64_t* __restrict__ labels,
+    float* __restrict__ lse_out, float* __restrict__ partial, int64_t B, int C) {
+  constexpr int R = rows_in_flight<V>();
+  constexpr int RPB = kBlock / TPR;
+  constexpr int RPI = RPB * R;
+  __shared__ float red[4 * R];
+  __shared__ float sacc[RPB];
+  const int t = threadIdx.x % TPR;
+  const int grp = threadIdx.x / TPR;
+  const int C4 = C >> 2;
+  float acc = 0.f;
+  for (int64_t base = (int64_t)blockIdx.x * RPI; base < B; base += (int64_t)gridDim.x * RPI) {
+    f32x4 v[R][V];
+    int64_t lab[R];
+    float xl[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) lab[r] = labels[min(base + r * RPB + grp, B - 1)];
+    // the scheduler must not pull the label arithmetic between these loads
+    // (it would wait for the labels before issuing the rows)
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const f32x4* xr =
+          reinterpret_cast<const f32x4*>(logits + min(base + r * RPB + grp, B - 1) * C);
+#pragma unroll
+      for (int k = 0; k < V; ++k) v[r][k] = xr[FULL ? t + k * TPR : min(t + k * TPR, C4 - 1)];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // the label's logit, addressed by the labels loaded first (column 0 for
+    // an invalid label, whose term becomes NaN below)
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      xl[r] = logits[min(base + r * RPB + grp, B - 1) * C + max(label_col(lab[r], C), 0)];
+    // keep every load above any use of the row data
+    __builtin_amdgcn_sched_barrier(0);
+    float m[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      m[r] = -INFINITY;
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        const bool ok = FULL || t + k * TPR < C4;
+        const f32x4 x = v[r][k];
+        const float mk = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+        m[r] = fmaxf(m[r], ok ? mk : -INFINITY);
+      }
+    }
+    row_reduce<TPR, R, true>(m, red);
+    float se[R];  // per row: sum of exp(x - max)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      se[r] = 0.f;
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        float e4 = 0.f;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) e4 += __builtin_amdgcn_exp2f((v[r][k][u] - m[r]) * kLog2e);
+        se[r] += (FULL || t + k * TPR < C4) ? e4 : 0.f;
+      }
+    }
+    row_reduce<TPR, R, false>(se, red);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t row = base + r * RPB + grp;
+      const float lse = m[r] + __builtin_amdgcn_logf(se[r]) * kLn2;
+      const float term = label_col(lab[r], C) >= 0 ? lse - xl[r] : NAN;
+      const bool mine = row < B && t == 0;
+      // a select, not a branch: a branch would let the compiler sink the
+      // label and logit loads into it, after all the row work
+      acc += mine ? term : 0.f;
+      if (mine) lse_out[row] = lse;
+    }
+  }
+  if (t == 0) sacc[grp] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float wg = 0.f;
+#pragma unroll
+    for (int g = 0; g < RPB; ++g) wg += sacc[g];
+    partial[blockIdx.x] = wg;
+  }
+}
+
+// Generic forward (any C and alignment): workgroups stride over the rows,
+// one row at a time, three passes over it (max, sum of exp) from L2.
+__global__ __launch_bounds__(kBlock) void sce_fwd_generic_kernel(
+    const float* __restrict__ logits, const int64_t* __restrict__ labels,
+    float* __restrict__ lse_out, float* __restrict__ partial, int64_t B, int64_t C) {
+  __shared__ float red[4];
+  float acc = 0.f;
+  for (int64_t row = blockIdx.x; row < B; row += gridDim.x) {
+    const float* xr = logits + row * C;
+    float m[1] = {-INFINITY};
+    for (int64_t c = threadIdx.x; c < C; c += kBlock) m[0] = fmaxf(m[0], xr[c]);
+    row_reduce<kBlock, 1, true>(m, red);
+    float se[1] = {0.f};
+    for (int64_t c = threadIdx.x; c < C; c += kBlock)
+      se[0] += __builtin_amdgcn_exp2f((xr[c] - m[0]) * kLog2e);
+    row_reduce<kBlock, 1, false>(se, red);
+    if (threadIdx.x == 0) {
+      const float lse = m[0] + __builtin_amdgcn_logf(se[0]) * kLn2;
+      const int lab = label_col(labels[row], C);
+      lse_out[row] = lse;
+      acc += lab >= 0 ? lse - xr[lab] : NAN;
+    }
+  }
+  if (threadIdx.x == 0) partial[blockIdx.x] = acc;
+}
+
+// loss = (sum of the n <= kFwdBlocks partials, added in a fixed order) / B.
+// Every thread issues its kFwdBlocks / kBlock loads (clamped addresses)
+// before adding any, so the kernel waits for one memory round trip.
+__global__ __launch_bounds__(kBlock) void sce_finalize_kernel(const float* __restrict__ partial,
+                                                              int n, int64_t B,
+                                                              float* __restrict__ loss) {
+  constexpr int kPer = kFwdBlocks / kBlock;
+  __shared__ float red[4];
+  float x[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) x[j] = partial[min((int)threadIdx.x + j * kBlock, n - 1)];
+  float s[1] = {0.f};
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) s[0] += (int)threadIdx.x + j * kBlock < n ? x[j] : 0.f;
+  row_reduce<kBlock, 1, false>(s, red);
+  if (threadIdx.x == 0) loss[0] = s[0] / (float)B;
+}
+
+// Row-cached backward, laid out like the forward: TPR threads per row, V
+// float4 per thread, R rows' loads issued before any is used.  Per row,
+// scale = gout / B (NaN for an invalid label); dlogits = scale * exp(x - lse)
+// everywhere, then the thread holding the label's column subtracts scale
+// there.
+template <int TPR, int V, bool FULL>
+__global__ __launch_bounds__(kBlock) void sce_bwd_rows_kernel(
+    const float* __restrict__ logits, const int64_t* __restrict__ labels,
+    const float* __restrict__ lse, const float* __restrict__ gout,
+    float* __restrict__ dlogits, int64_t B, int C) {
+  constexpr int R = rows_in_flight<V>();
+  constexpr int RPB = kBlock / TPR;
+  constexpr int RPI = RPB * R;
+  const int t = threadIdx.x % TPR;
+  const int grp = threadIdx.x / TPR;
+  const int C4 = C >> 2;
+  const float g = gout[0] / (float)B;
+  for (int64_t base = (int64_t)blockIdx.x * RPI; base < B; base += (int64_t)gridDim.x * RPI) {
+    f32x4 v[R][V];
+    int64_t lab[R];
+    float l[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t row = min(base + r * RPB + grp, B - 1);
+      lab[r] = labels[row];
+      l[r] = lse[row];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const f32x4* xr =
+          reinterpret_cast<const f32x4*>(logits + min(base + r * RPB + grp, B - 1) * C);
+#pragma unroll
+      for (int k = 0; k < V; ++k) v[r][k] = xr[FULL ? t + k * TPR : min(t + k * TPR, C4 - 1)];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // Rows past B were loaded as row B - 1, so their results are row B - 1's,
+    // bit for bit: they are stored there again (identical values from the
+    // same instructions) rather than behind a branch, which would let the
+    // compiler sink the loads of the last rows into it.
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t row = min(base + r * RPB + grp, B - 1);
+      const int lc = label_col(lab[r], C);
+      const float scale = lc >= 0 ? g : NAN;
+      f32x4* dr = reinterpret_cast<f32x4*>(dlogits + row * C);
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        // columns past the row were loaded as its last float4: the same
+        // holds for them (their results are the last float4's, stored again)
+        const int c = FULL ? t + k * TPR : min(t + k * TPR, C4 - 1);
+        // scale at the label's column (never for lc = -1), else 0
+        const float hit = c == (lc >> 2) ? scale : 0.f;
+        f32x4 o;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          o[u] = fmaf(scale, __builtin_amdgcn_exp2f((v[r][k][u] - l[r]) * kLog2e),
+                      u == (lc & 3) ? -hit : 0.f);
+        dr[c] = o;
+      }
+    }
+  }
+}
+
+// Flat backward for the shapes the row-cached kernel does not take:
+// dlogits = gout / B * (exp(x - lse) - onehot); VEC: C % 4 == 0 and aligned
+// rows, one float4 per thread step.
+template <bool VEC>
+__global__ __launch_bounds__(kBlock) void sce_bwd_kernel(
+    const float* __restrict__ logits, const int64_t* __restrict__ labels,
+    const float* __restrict__ lse, const float* __restrict__ gout,
+    float* __restrict__ dlogits, int64_t B, int64_t C) {
+  const float scale = gout[0] / (float)B;
+  const int64_t W = VEC ? C / 4 : C;
+  const int64_t n = B * W;
+  for (int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x; e < n;
+       e += (int64_t)gridDim.x * kBlock) {
+    const int64_t row = e / W;
+    const int64_t c0 = (e - row * W) * (VEC ? 4 : 1);
+    const float l = lse[row];
+    const int lab = label_col(labels[row], C);
+    const float bad = lab >= 0 ? 0.f : NAN;
+    if (VEC) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(logits + row * C + c0);
+      f32x4 o;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        o[u] = scale * (__builtin_amdgcn_exp2f((x[u] - l) * kLog2e) -
+                        (c0 + u == lab ? 1.f : 0.f)) + bad;
+      *reinterpret_cast<f32x4*>(dlogits + row * C + c0) = o;
+    } else {
+      const float x = logits[row * C + c0];
+      dlogits[row * C + c0] =
+          scale * (__builtin_amdgcn_exp2f((x - l) * kLog2e) - (c0 == lab ? 1.f : 0.f)) + bad;
+    }
+  }
+}
+
+// ----------------------------------------------------------------- planning
+struct FwdPlan {
+  bool cached = false;
+  int tpr = 64, v = 4;
+  unsigned blocks = 1;  // forward workgroups, one partial loss each
+};
+
+FwdPlan plan_forward(int64_t B, int64_t C, bool aligned) {
+  FwdPlan p;
+  p.cached = aligned && C % 4 == 0 && C <= 8192;
+  int64_t rows_per_step = 1;
+  if (p.cached) {
+    const int64_t c4 = C / 4;
+    if (c4 <= 64) { p.tpr = 64; p.v = 1; }
+    else if (c4 <= 256) { p.tpr = 64; p.v = 4; }
+    else { p.tpr = 256; p.v = c4 <= 512 ? 2 : c4 <= 1024 ? 4 : 8; }
+    const int r = p.v == 1 ? rows_in_flight<1>() : p.v == 2 ? rows_in_flight<2>()
+                                                            : rows_in_flight<4>();
+    rows_per_step = (kBlock / p.tpr) * r;
+  }
+  // B == 0 still runs one workgroup: its partial is 0 and the finalize
+  // writes loss = 0 / 0 = NaN (the mean of no terms, as torch's mean of an
+  // empty tensor)
+  p.blocks = (unsigned)std::max<int64_t>(1, std::min<int64_t>(kFwdBlocks,
+                                                             nl2k::ceil_div(B, rows_per_step)));
+  return p;
+}
+
+int validate(int64_t B, int64_t C, const char* who) {
+  if (B < 0 || C < 1)
+    return nl2k::fail(NL2K_ERR_SHAPE, "%s: need B >= 0 and C >= 1 (got B=%lld C=%lld)", who,
+                      (long long)B, (long long)C);
+  if (B > INT32_MAX || C > INT32_MAX || B > INT64_MAX / C)
+    return nl2k::fail(NL2K_ERR_OVERFLOW, "%s: sizes too large (B=%lld C=%lld)", who,
+                      (long long)B, (long long)C);
+  return NL2K_SUCCESS;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* softmax_ce_last_error(void) { return nl2k::error_slot().text; }
+
+size_t softmax_ce_forward_workspace_bytes(int64_t B, int64_t C) {
+  if (validate(B, C, "softmax_ce_forward_workspace_bytes")) return 0;
+  return kWorkspaceBytes;
+}
+
+int softmax_ce_forward_f32(const float* logits, const int64_t* labels, float* loss, float* lse,
+                           int64_t B, int64_t C, void* workspace, size_t workspace_bytes,
+                           hipStream_t stream) {
+  const char* who = "softmax_ce_forward_f32";
+  int st = validate(B, C, who);
+  if (st) return st;
+  if (!loss || (B > 0 && (!logits || !labels || !lse)))
+    return nl2k::fail(NL2K_ERR_NULL, "%s: null pointer argument", who);
+  if (!workspace || workspace_bytes < kWorkspaceBytes)
+    return nl2k::fail(NL2K_ERR_WORKSPACE, "%s: workspace of %zu bytes required, got %zu", who,
+                      kWorkspaceBytes, workspace ? workspace_bytes : (size_t)0);
+  if (reinterpret_cast<uintptr_t>(workspace) % 4 != 0)
+    return nl2k::fail(NL2K_ERR_ALIGN, "%s: workspace must be 4-byte aligned", who);
+  float* partial = static_cast<float*>(workspace);
+  const FwdPlan p = plan_forward(B, C, nl2k::aligned16(logits));
+  const dim3 grid(p.blocks);
+  if (p.cached && B > 0) {
+#define SCE_FWD(TPR, V)                                                                        \
+  do {                                                                                         \
+    if (C / 4 == (TPR) * (V))                                                                  \
+      hipLaunchKernelGGL((sce_fwd_kernel<TPR, V, true>), grid, dim3(kBlock), 0, stream, logits, \
+                         labels, lse, partial, B, (int)C);                                     \
+    else                                                                                       \
+      hipLaunchKernelGGL((sce_fwd_kernel<TPR, V, false>), grid, dim3(kBlock), 0, stream,       \
+                         logits, labels, lse, partial, B, (int)C);                             \
+  } while (0)
+    if (p.tpr == 64 && p.v == 1) SCE_FWD(64, 1);
+    else if (p.tpr == 64) SCE_FWD(64, 4);
+    else if (p.v == 2) SCE_FWD(256, 2);
+    else if (p.v == 4) SCE_FWD(256, 4);
+    else SCE_FWD(256, 8);
+#undef SCE_FWD
+  } else {
+    hipLaunchKernelGGL(sce_fwd_generic_kernel, grid, dim3(kBlock), 0, stream, logits, labels, lse,
+                       partial, B, C);
+  }
+  st = nl2k::check_launch(who);
+  if (st) return st;
+  hipLaunchKernelGGL(sce_finalize_kernel, dim3(1), dim3(kBlock), 0, stream, partial,
+                     (int)p.blocks, B, loss);
+  return nl2k::check_launch(who);
+}
+
+int softmax_ce_backward_f32(const float* logits, const int64_t* labels, const float* lse,
+                            const float* gout, float* dlogits, int64_t B, int64_t C,
+                            hipStream_t stream) {
+  const char* who = "softmax_ce_backward_f32";
+  int st = validate(B, C, who);
+  if (st) return st;
+  if (B == 0) return nl2k::succeed();
+  if (!logits || !labels || !lse || !gout || !dlogits)
+    return nl2k::fail(NL2K_ERR_NULL, "%s: null pointer argument", who);
+  const bool aligned = nl2k::aligned16(logits) && nl2k::aligned16(dlogits);
+  const FwdPlan p = plan_forward(B, C, aligned);
+  if (p.cached) {
+    const dim3 grid(p.blocks);
+#define SCE_BWD(TPR, V)                                                                      \
+  do {                                                                                       \
+    if (C / 4 == (TPR) * (V))                                                                \
+      hipLaunchKernelGGL((sce_bwd_rows_kernel<TPR, V, true>), grid, dim3(kBlock), 0, stream, \
+                         logits, labels, lse, gout, dlogits, B, (int)C);                     \
+    else                                                                                     \
+      hipLaunchKernelGGL((sce_bwd_rows_kernel<TPR, V, false>), grid, dim3(kBlock), 0, stream, \
+                         logits, labels, lse, gout, dlogits, B, (int)C);                     \
+  } while (0)
+    if (p.tpr == 64 && p.v == 1) SCE_BWD(64, 1);
+    else if (p.tpr == 64) SCE_BWD(64, 4);
+    else if (p.v == 2) SCE_BWD(256, 2);
+    else if (p.v == 4) SCE_BWD(256, 4);
+    else SCE_BWD(256, 8);
+#undef SCE_BWD
+  } else {
+    const bool vec = C % 4 == 0 && aligned;
+    const int64_t work = vec ? B * C / 4 : B * C;
+    const unsigned grid = (unsigned)std::min<int64_t>(nl2k::ceil_div(work, kBlock), 8192);
+    if (vec)
+      hipLaunchKernelGGL(sce_bwd_kernel<true>, dim3(grid), dim3(kBlock), 0, stream, logits,
+                         labels, lse, gout, dlogits, B, C);
+    else
+      hipLaunchKernelGGL(sce_bwd_kernel<false>, dim3(grid), dim3(kBlock), 0, stream, logits,
+                         labels, lse, gout, dlogits, B, C);
+  }
+  return nl2k::check_launch(who);
+}
+
+}  // extern "C"

@@ -1,5 +1,5 @@
 """Roofline report for the follow-on cases (layernorm, l2norm_scale, scan,
-spmv, cosine_sim) on one GPU.
+spmv, cosine_sim, softmax_ce) on one GPU.
 
 For each case's acceptance workload this times every C-ABI entry point
 directly on preallocated device buffers: a 512 MiB read flush before each
@@ -13,7 +13,7 @@ launch (a few us); rocprofv3 kernel times (framework/profile.py stats) give
 the kernel-only figure.
 
 Usage:  python nl2cuda-kernel-agent_amd/framework/roofline.py
-            [--case all|layernorm|l2norm|scan|spmv|cosine]
+            [--case all|layernorm|l2norm|scan|spmv|cosine|softmax_ce]
 Prints one JSON line per measurement and a closing table.
 """
 
@@ -124,6 +124,39 @@ def l2norm(dev, time_us):
     return out
 
 
+def softmax_ce(dev, time_us):
+    """Softmax cross-entropy (HBM-bound): forward reads logits and labels,
+    writes lse and the loss; backward reads logits, labels, lse and gout,
+    writes dlogits.  The forward's scratch (one partial per workgroup, 4 KiB)
+    is not counted."""
+    import torch
+    from framework import capi
+    from cases.softmax_ce import op, config
+    lib = op._lib()
+    out = []
+    for B, C in config.BENCH_SHAPES:
+        gen = torch.Generator().manual_seed(0)
+        x = torch.randn(B, C, generator=gen).to(dev)
+        lab = torch.randint(0, C, (B,), generator=gen).to(dev)
+        dx = torch.empty_like(x)
+        loss, lse = torch.empty(1, device=dev), torch.empty(B, device=dev)
+        gout = torch.ones(1, device=dev)
+        wsb = lib.softmax_ce_forward_workspace_bytes(B, C)
+        ws = torch.empty(max(wsb // 4, 1), device=dev)
+        s, P = capi.stream_of(x), capi.ptr
+        t = time_us(lambda: _check(lib.softmax_ce_forward_f32(P(x), P(lab), P(loss), P(lse), B, C,
+                                                              P(ws), wsb, s),
+                                   lib, "softmax_ce_last_error"))
+        out.append(("softmax_ce", f"forward_f32 [{B},{C}]", t, 4 * B * C + 12 * B + 4,
+                    "read logits, labels; write lse, loss"))
+        t = time_us(lambda: _check(lib.softmax_ce_backward_f32(P(x), P(lab), P(lse), P(gout), P(dx),
+                                                               B, C, s),
+                                   lib, "softmax_ce_last_error"))
+        out.append(("softmax_ce", f"backward_f32 [{B},{C}]", t, 8 * B * C + 12 * B + 4,
+                    "read logits, labels, lse, gout; write dlogits"))
+    return out
+
+
 def scan(dev, time_us, shapes=SCAN_SHAPES):
     import torch
     from framework import capi
@@ -138,7 +171,7 @@ def scan(dev, time_us, shapes=SCAN_SHAPES):
         y64 = torch.empty(R, D, dtype=torch.int64, device=dev)
         y32 = torch.empty_like(xi)
         wsb = lib.scan_workspace_bytes(R, D)
-        ws = torch.zeros(max(wsb // 8, 1), dtype=torch.int64, device=dev)  # zeroed once
+        ws = torch.empty(max(wsb // 4, 1), device=dev)  # zeroed once
         s, P = capi.stream_of(x), capi.ptr
         shape = f"[{R},{D}]"
         for name, fn, nbytes, what in (
@@ -224,7 +257,8 @@ def cosine(dev, time_us):
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--case", default="all",
-                    choices=["all", "layernorm", "l2norm", "scan", "spmv", "cosine"])
+                    choices=["all", "layernorm", "l2norm", "scan", "spmv", "cosine",
+                             "softmax_ce"])
     ap.add_argument("--iters", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--scan-shape", default=None, metavar="RxD",
@@ -239,7 +273,8 @@ def main(argv=None):
         r, d = (int(v) for v in ns.scan_shape.lower().split("x"))
         scan_shapes = ((r, d),)
     cases = {"layernorm": layernorm, "l2norm": l2norm,
-             "scan": lambda dv, t: scan(dv, t, scan_shapes), "spmv": spmv, "cosine": cosine}
+             "scan": lambda dv, t: scan(dv, t, scan_shapes), "spmv": spmv, "cosine": cosine,
+             "softmax_ce": softmax_ce}
     rows = []
     for name in (cases if ns.case == "all" else [ns.case]):
         for case, what, t, nbytes, detail, *flops in cases[name](dev, time_us):

@@ -18,7 +18,8 @@ INCLUDE = os.path.join(REPO, "include")
 # header -> op module that loads the library implementing it
 HEADERS = {"rbf.h": "cases.rbf.op", "layernorm.h": "cases.layernorm.op",
            "scan.h": "cases.scan.op", "spmv.h": "cases.spmv.op",
-           "cosine_sim.h": "cases.cosine_sim.op", "l2norm_scale.h": "cases.l2norm_scale.op"}
+           "cosine_sim.h": "cases.cosine_sim.op", "l2norm_scale.h": "cases.l2norm_scale.op",
+           "softmax_ce.h": "cases.softmax_ce.op"}
 
 STATUS = {}
 with open(os.path.join(INCLUDE, "nl2k_status.h")) as _f:
@@ -199,6 +200,32 @@ def test_l2norm_scale_argument_validation_without_gpu():
     st = lib.l2norm_scale_backward_f32(fake, fake, fake, fake, fake, fake, 16384, 1024, fake,
                                        need - 4, None)
     assert st == STATUS["NL2K_ERR_WORKSPACE"]
+
+
+def test_softmax_ce_argument_validation_without_gpu():
+    lib = _load("cases.softmax_ce.op")
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: every call below fails validation
+    # one partial loss for each of at most 1024 workgroups
+    assert lib.softmax_ce_forward_workspace_bytes(8192, 1024) == 4 * 1024
+    assert lib.softmax_ce_forward_workspace_bytes(0, 1024) == 4 * 1024
+    assert lib.softmax_ce_forward_workspace_bytes(-1, 1024) == 0
+    need = 4 * 1024
+    st = lib.softmax_ce_forward_f32(fake, fake, fake, fake, -1, 1024, fake, need, None)
+    assert st == STATUS["NL2K_ERR_SHAPE"]
+    st = lib.softmax_ce_forward_f32(fake, fake, fake, fake, 8, 0, fake, need, None)
+    assert st == STATUS["NL2K_ERR_SHAPE"]
+    st = lib.softmax_ce_forward_f32(fake, None, fake, fake, 8, 16, fake, need, None)
+    assert st == STATUS["NL2K_ERR_NULL"]
+    st = lib.softmax_ce_forward_f32(fake, fake, fake, fake, 8192, 1024, fake, need - 4, None)
+    assert st == STATUS["NL2K_ERR_WORKSPACE"] and b"workspace" in lib.softmax_ce_last_error()
+    odd = ctypes.c_void_p((1 << 20) + 2)
+    st = lib.softmax_ce_forward_f32(fake, fake, fake, fake, 8192, 1024, odd, need, None)
+    assert st == STATUS["NL2K_ERR_ALIGN"]
+    st = lib.softmax_ce_backward_f32(fake, fake, fake, None, fake, 8, 16, None)
+    assert st == STATUS["NL2K_ERR_NULL"]
+    st = lib.softmax_ce_backward_f32(fake, fake, fake, fake, fake, 1 << 31, 16, None)
+    assert st == STATUS["NL2K_ERR_OVERFLOW"]
+    assert lib.softmax_ce_backward_f32(None, None, None, None, None, 0, 16, None) == 0
 
 
 DELIVERY = os.path.join(REPO, "nl2cuda-kernel-agent_amd", "cases", "rbf", "delivery")
