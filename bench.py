@@ -177,6 +177,24 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
 
+    # End-to-end RBFFunction forward + backward through autograd (the case's
+    # candidate), after and outside the timed region: the C-ABI calls above
+    # plus torch's output allocations and the autograd engine.
+    e2e_ms = []
+    Xa = X.detach().clone().requires_grad_(True)
+    Ya = Y.detach().clone().requires_grad_(True)
+    for i in range(min(args.steps, 10) + 2):
+        flush_caches(dev)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        op.candidate({"X": Xa, "Y": Ya}, {"gamma": gamma}).backward(dK)
+        b.record(stream)
+        torch.cuda.synchronize()
+        if i >= 2:
+            e2e_ms.append(a.elapsed_time(b))
+        Xa.grad = Ya.grad = None
+    e2e_ms.sort()
+
     fwd_ms = [a.elapsed_time(b) for a, b, _ in events]
     bwd_ms = [b.elapsed_time(c) for _, b, c in events]
     fwd_avg = sum(fwd_ms) / len(fwd_ms)
@@ -221,6 +239,7 @@ def main():
         "fwd_gbs": round(fb / (fwd_avg * 1e-3) / 1e9, 1),
         "bwd_gbs": round(bb / (bwd_avg * 1e-3) / 1e9, 1),
         "pct_hbm_roofline": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "e2e_autograd_us": round(e2e_ms[len(e2e_ms) // 2] * 1e3, 2),
         "fwd_tflops": round(fwd_tf, 2),
         "bwd_tflops": round(bwd_tf, 2),
         "pct_fp32_roofline": round(100 * (ff + bf) / (step_ms * 1e-3) / 1e12 / FP32_PEAK_TFLOPS, 2),

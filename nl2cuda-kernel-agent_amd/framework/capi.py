@@ -16,6 +16,7 @@ c_int64 = ctypes.c_int64
 c_int = ctypes.c_int
 c_float = ctypes.c_float
 c_size_t = ctypes.c_size_t
+c_double = ctypes.c_double
 
 
 def bind(lib, name, argtypes, restype=ctypes.c_int):

@@ -1,0 +1,142 @@
+// Peak-rate microbenchmarks for one MI355X (gfx950): the HBM stream rates
+// (read, write, copy of float4) and the fp32 MFMA rate with the shader
+// clock it ran at.  They confirm, on the box, the published peaks the
+// roofline fractions are priced against (8 TB/s HBM, 157.3 TFLOP/s fp32
+// matrix).  C-ABI; no state; launches on `stream`.
+#include <algorithm>
+#include <cstdint>
+
+#include "common.h"
+
+using nl2k::f32x4;
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kChains = 8;  // independent MFMA accumulators per wave
+
+// Grid-stride read of n4 float4, U loads in flight per thread step; each
+// workgroup writes one sum to sink[blockIdx.x] so the loads stay live.
+template <int U>
+__global__ __launch_bounds__(kBlock) void peak_read_kernel(const f32x4* __restrict__ src,
+                                                           int64_t n4, float* __restrict__ sink) {
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  f32x4 acc = nl2k::zero4();
+  for (; i + (U - 1) * stride < n4; i += U * stride) {
+    f32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = src[i + u * stride];
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc += v[u];
+  }
+  for (; i < n4; i += stride) acc += src[i];
+  float s = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  s = nl2k::wave_sum_dpp(s);
+  if (threadIdx.x == 0) sink[blockIdx.x] = s;  // one wave's sum is enough to keep the loads
+}
+
+__global__ __launch_bounds__(kBlock) void peak_write_kernel(f32x4* __restrict__ dst, int64_t n4,
+                                                            float v) {
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride)
+    dst[i] = f32x4{v, v, v, v};
+}
+
+__global__ __launch_bounds__(kBlock) void peak_copy_kernel(const f32x4* __restrict__ src,
+                                                           f32x4* __restrict__ dst, int64_t n4) {
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  for (; i + stride < n4; i += 2 * stride) {
+    const f32x4 a = src[i], b = src[i + stride];
+    dst[i] = a;
+    dst[i + stride] = b;
+  }
+  for (; i < n4; i += stride) dst[i] = src[i];
+}
+
+// iters (even) x kChains independent v_mfma_f32_16x16x4f32 per wave (2048
+// flops each).  Workgroup 0's first lane records the shader-clock ticks
+// (s_memtime) and the 100 MHz real-time ticks (s_memrealtime) of its loop.
+__global__ __launch_bounds__(kBlock) void peak_mfma_f32_kernel(float* __restrict__ out,
+                                                               unsigned long long* __restrict__ clk,
+                                                               int iters) {
+  f32x4 acc[kChains];
+#pragma unroll
+  for (int j = 0; j < kChains; ++j) acc[j] = nl2k::zero4();
+  const float a = 1e-3f * (float)(threadIdx.x & 63), b = 1.0f - 1e-4f * (float)(threadIdx.x & 7);
+  const unsigned long long t0 = __builtin_amdgcn_s_memtime();
+  const unsigned long long r0 = __builtin_amdgcn_s_memrealtime();
+  // unrolled by two: a single-step body gets accumulator copies (VALU work
+  // between the MFMAs) from the register allocator
+  for (int it = 0; it < iters; it += 2) {
+#pragma unroll
+    for (int j = 0; j < kChains; ++j) acc[j] = nl2k::mfma16x4(a, b, acc[j]);
+#pragma unroll
+    for (int j = 0; j < kChains; ++j) acc[j] = nl2k::mfma16x4(b, a, acc[j]);
+  }
+  const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+  const unsigned long long r1 = __builtin_amdgcn_s_memrealtime();
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < kChains; ++j) s += (acc[j][0] + acc[j][1]) + (acc[j][2] + acc[j][3]);
+  out[(int64_t)blockIdx.x * kBlock + threadIdx.x] = s;
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    clk[0] = t1 - t0;
+    clk[1] = r1 - r0;
+  }
+}
+
+bool bad_stream_args(int64_t n4, int blocks) { return n4 < 1 || blocks < 1 || blocks > (1 << 20); }
+
+}  // namespace
+
+extern "C" {
+
+const char* peaks_last_error(void) { return nl2k::error_slot().text; }
+
+// Stream kernels on `blocks` workgroups of 256 threads.  The read's `sink`
+// holds `blocks` floats; `unroll` (4 or 8) is its loads in flight per step.
+int peaks_read_f32x4(const float* src, int64_t n4, float* sink, int blocks, int unroll,
+                     hipStream_t stream) {
+  if (bad_stream_args(n4, blocks) || !src || !sink || (unroll != 4 && unroll != 8))
+    return nl2k::fail(NL2K_ERR_SHAPE, "peaks_read_f32x4: bad arguments");
+  const f32x4* p = reinterpret_cast<const f32x4*>(src);
+  if (unroll == 4)
+    hipLaunchKernelGGL(peak_read_kernel<4>, dim3(blocks), dim3(kBlock), 0, stream, p, n4, sink);
+  else
+    hipLaunchKernelGGL(peak_read_kernel<8>, dim3(blocks), dim3(kBlock), 0, stream, p, n4, sink);
+  return nl2k::check_launch("peaks_read_f32x4");
+}
+
+int peaks_write_f32x4(float* dst, int64_t n4, int blocks, hipStream_t stream) {
+  if (bad_stream_args(n4, blocks) || !dst)
+    return nl2k::fail(NL2K_ERR_SHAPE, "peaks_write_f32x4: bad arguments");
+  hipLaunchKernelGGL(peak_write_kernel, dim3(blocks), dim3(kBlock), 0, stream,
+                     reinterpret_cast<f32x4*>(dst), n4, 1.0f);
+  return nl2k::check_launch("peaks_write_f32x4");
+}
+
+int peaks_copy_f32x4(const float* src, float* dst, int64_t n4, int blocks, hipStream_t stream) {
+  if (bad_stream_args(n4, blocks) || !src || !dst)
+    return nl2k::fail(NL2K_ERR_SHAPE, "peaks_copy_f32x4: bad arguments");
+  hipLaunchKernelGGL(peak_copy_kernel, dim3(blocks), dim3(kBlock), 0, stream,
+                     reinterpret_cast<const f32x4*>(src), reinterpret_cast<f32x4*>(dst), n4);
+  return nl2k::check_launch("peaks_copy_f32x4");
+}
+
+// Flops one peaks_mfma_f32 launch performs.
+double peaks_mfma_f32_flops(int blocks, int iters) {
+  return (double)blocks * (kBlock / 64) * iters * kChains * 2.0 * 16 * 16 * 4;
+}
+
+// out: blocks * 256 floats; clk: 2 values (shader-clock ticks, 100 MHz ticks).
+int peaks_mfma_f32(float* out, unsigned long long* clk, int blocks, int iters,
+                   hipStream_t stream) {
+  if (blocks < 1 || iters < 2 || iters % 2 != 0 || !out || !clk)
+    return nl2k::fail(NL2K_ERR_SHAPE, "peaks_mfma_f32: bad arguments");
+  hipLaunchKernelGGL(peak_mfma_f32_kernel, dim3(blocks), dim3(kBlock), 0, stream, out, clk, iters);
+  return nl2k::check_launch("peaks_mfma_f32");
+}
+
+}  // extern "C"

@@ -15,6 +15,10 @@ commit next to the code:
            give bytes-per-count factors, which turn the selected kernels'
            per-dispatch readings into HBM bytes per launch.  Writes
            <out>/<name>_traffic.json and .md.
+  mfma     one rocprofv3 --pmc pass of the derived counters MfmaUtil (the
+           MFMA pipes' busy cycles over all SIMDs and the GPU-active
+           cycles) and MfmaFlopsF32 (fp32 MFMA flops) for the selected
+           kernels, per dispatch.  Writes <out>/<name>_mfma.json and .md.
   run-case the profiled program for a case: warmup, then --iters steps of
            the case's candidate (forward only or forward+backward).
 
@@ -204,6 +208,52 @@ def cmd_traffic(ns, cmd):
     return 0
 
 
+MFMA_COUNTERS = ("MfmaUtil", "MfmaFlopsF32")
+
+
+def cmd_mfma(ns, cmd):
+    kernels = [k for k in ns.kernels.split(",") if k]
+    d = _rocprof(["--pmc"] + list(MFMA_COUNTERS), ns.raw, f"{ns.name}_mfma", cmd, ns.limit)
+    rows = counter_rows(d)
+    per_kernel = {}
+    for k in kernels:
+        entry = {}
+        for counter in MFMA_COUNTERS:
+            vals, _ = per_dispatch(rows, counter, [k])
+            if not vals:
+                raise RuntimeError(f"kernel {k} has no {counter} readings in {d}")
+            v = sorted(vals.values())
+            entry[counter] = {"dispatches": len(v), "median": v[len(v) // 2],
+                              "min": v[0], "max": v[-1]}
+        per_kernel[k] = entry
+    doc = {"name": ns.name, "kernels": kernels,
+           "command": " ".join(shlex.quote(c) for c in _INVOCATION),
+           "profiled": " ".join(shlex.quote(c) for c in cmd),
+           "counters": {"MfmaUtil": "percent: sum of SQ_VALU_MFMA_BUSY_CYCLES over SIMDs / "
+                                    "(GRBM_GUI_ACTIVE x SIMD count) x 100",
+                        "MfmaFlopsF32": "SQ_INSTS_VALU_MFMA_MOPS_F32 x 512 (fp32 MFMA flops)"},
+           "per_kernel": per_kernel}
+    os.makedirs(ns.out, exist_ok=True)
+    with open(os.path.join(ns.out, f"{ns.name}_mfma.json"), "w") as f:
+        json.dump(doc, f, indent=1)
+    lines = [f"# MFMA utilisation per dispatch: {ns.name}", "", "Command:", "", "```", doc["command"],
+             "```", "", "which ran one pass of:", "", "```",
+             f"rocprofv3 --pmc {' '.join(MFMA_COUNTERS)} --output-format csv -d <dir> -o run -- "
+             + doc["profiled"], "```", "",
+             "MfmaUtil = " + doc["counters"]["MfmaUtil"] + ".  MfmaFlopsF32 = " +
+             doc["counters"]["MfmaFlopsF32"] + ".", "",
+             "| kernel | dispatches | MfmaUtil % (median, min-max) | MfmaFlopsF32 per dispatch (median) |",
+             "|---|---:|---:|---:|"]
+    for k, e in per_kernel.items():
+        u, fl = e["MfmaUtil"], e["MfmaFlopsF32"]
+        lines.append(f"| `{k}` | {u['dispatches']} | {u['median']:.1f} ({u['min']:.1f}-{u['max']:.1f}) | "
+                     f"{fl['median']:,.0f} |")
+    with open(os.path.join(ns.out, f"{ns.name}_mfma.md"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+    return 0
+
+
 def cmd_run_case(ns):
     """The profiled program: the case's candidate, like profile_case.py:48-78."""
     sys.path.insert(0, PKG)
@@ -249,7 +299,7 @@ def main(argv=None):
         argv, cmd = argv[:k], argv[k + 1:]
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     sub = ap.add_subparsers(dest="what", required=True)
-    for name in ("stats", "traffic"):
+    for name in ("stats", "traffic", "mfma"):
         p = sub.add_parser(name)
         p.add_argument("--name", required=True)
         p.add_argument("--out", default=os.path.join(REPO, "profiles"))
@@ -258,7 +308,7 @@ def main(argv=None):
         p.add_argument("--case", default=None, help="profile run-case for this case instead of a command")
         p.add_argument("--mode", choices=["forward", "both"], default="both")
         p.add_argument("--iters", type=int, default=50)
-        if name == "traffic":
+        if name in ("traffic", "mfma"):
             p.add_argument("--kernels", required=True, help="comma-separated kernel-name substrings")
     p = sub.add_parser("run-case")
     p.add_argument("--case", required=True)
@@ -273,7 +323,7 @@ def main(argv=None):
                "--mode", ns.mode, "--iters", str(ns.iters)]
     if not cmd:
         ap.error("give a command after -- or --case")
-    return cmd_stats(ns, cmd) if ns.what == "stats" else cmd_traffic(ns, cmd)
+    return {"stats": cmd_stats, "traffic": cmd_traffic, "mfma": cmd_mfma}[ns.what](ns, cmd)
 
 
 if __name__ == "__main__":
