@@ -32,11 +32,14 @@ extern "C" {
 #endif
 
 /* Workspace bytes any scan_* call below needs for [rows, D] (0 when every
- * row fits one chunk).  The workspace must be zero-filled once, before its
- * first use, and kept between calls: each call leaves it zeroed again (a
- * call is a single kernel launch, with no reset pass).  Calls that share a
- * workspace must not overlap in time; calls on different streams need
- * different workspaces.  A larger workspace serves smaller shapes too. */
+ * row fits one chunk).  The workspace needs no initial contents and no
+ * clearing: each call tags what it writes with a fresh 64-bit nonce and
+ * reads back only its own words (a word pair left by an earlier call, or a
+ * zero-filled one, is never taken; other contents pass the check only by
+ * chance, with probability 2^-64 per read), so a call is a single kernel
+ * launch.  Calls that share a workspace must not overlap in time; calls on
+ * different streams need different workspaces.  A larger workspace serves
+ * smaller shapes too. */
 size_t scan_workspace_bytes(int64_t rows, int64_t D);
 
 /* float32 -> float32 inclusive scan (scan.cu:83-95, `scan_forward`). */

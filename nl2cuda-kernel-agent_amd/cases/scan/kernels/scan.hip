@@ -28,14 +28,19 @@
 //    is capped so that every workgroup is resident, and each workgroup walks
 //    its chunks in increasing order and publishes before it waits, so the
 //    lowest unpublished chunk can always make progress.
-//  * The workspace cleans itself, so a call is a single launch: a slot holds
-//    its value XOR a bit pattern no total ever has, so an all-zero slot reads
-//    as "not yet published"; once every chunk of a row has read its carry
-//    (a per-row counter in the workspace), the last one zeroes the row's
-//    slots and the counter.  The caller zero-fills a workspace once, before
-//    its first use, and keeps it between calls.
+//  * Slots need no clearing, so a call is a single launch and the workspace
+//    needs no initial contents: every call draws a fresh 64-bit nonce n on
+//    the host (a process-wide counter, never 0) and two masks m0 and
+//    m1 = m0 ^ n; a slot is two words, v ^ m0 and v ^ m1, each written with
+//    one relaxed agent-scope atomic store.  A reader accepts the pair only
+//    when the two words XOR to n: a slot left complete by an earlier call
+//    XORs to that call's nonce and a zeroed one to 0, so neither passes; a
+//    pair read half-written, or never-written memory, passes only by chance
+//    (probability 2^-64 per read, as the masks are hashes of n).
 //  * Reverse scans mirror the positions: logical p <-> physical D - 1 - p.
 #include <algorithm>
+#include <atomic>
+#include <chrono>
 #include <cstdint>
 
 #include "../../../csrc/common.h"
@@ -57,29 +62,9 @@ constexpr int kResidentBlocks = 1024;           // 256 CUs x 4 workgroups
 constexpr unsigned kSpinLimit = 1u << 24;       // hang guard for the carry wait
 
 // ------------------------------------------------ 64-bit accumulator helpers
-template <typename Acc>
-struct Slot;
-// A published slot holds the total's bits XOR kMask; kMask itself is a bit
-// pattern no total has, so the stored word is never 0 and 0 means "empty".
-template <>
-struct Slot<double> {
-  // No double computed from float inputs has all 52 mantissa bits set.
-  static constexpr unsigned long long kMask = ~0ull;
-  __device__ static unsigned long long enc(double v) {
-    unsigned long long b = __builtin_bit_cast(unsigned long long, v);
-    if (b == kMask) b = 0x7FF8000000000000ull;  // a NaN with that payload: canonical NaN
-    return b ^ kMask;
-  }
-  __device__ static double dec(unsigned long long w) {
-    return __builtin_bit_cast(double, w ^ kMask);
-  }
-};
-template <>
-struct Slot<int64_t> {
-  // |sum| <= D * 2^31 <= 2^62, so INT64_MIN never occurs.
-  static constexpr unsigned long long kMask = 0x8000000000000000ull;
-  __device__ static unsigned long long enc(int64_t v) { return (unsigned long long)v ^ kMask; }
-  __device__ static int64_t dec(unsigned long long w) { return (int64_t)(w ^ kMask); }
+// The call's slot masks (m1 = m0 ^ nonce).
+struct SlotKey {
+  unsigned long long m0, m1;
 };
 
 template <typename T>
@@ -248,28 +233,41 @@ __device__ __forceinline__ void emit_tile(const TileScan<In, Acc>& s, Acc base, 
   }
 }
 
+// Publishes a chunk total in slot pair p (two words, see the header).
+template <typename Acc>
+__device__ __forceinline__ void publish(unsigned long long* __restrict__ slots, int p, Acc v,
+                                        SlotKey key) {
+  const unsigned long long b = bits64(v);
+  __hip_atomic_store(slots + 2 * p, b ^ key.m0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(slots + 2 * p + 1, b ^ key.m1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Sum of the totals of chunks [0, chunk) of a row, in a fixed order (wave 0).
 template <typename Acc>
 __device__ Acc carry_in(const unsigned long long* __restrict__ slots, int chunk, int lane,
-                        unsigned* __restrict__ err) {
+                        SlotKey key, unsigned* __restrict__ err) {
+  const unsigned long long tag = key.m0 ^ key.m1;  // the call's nonce
   Acc carry = (Acc)0;
   for (int base = 0; base < chunk; base += 64) {
     const int p = base + lane;
     Acc v = (Acc)0;
     if (p < chunk) {
-      unsigned long long b =
-          __hip_atomic_load(slots + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      unsigned long long w0 =
+          __hip_atomic_load(slots + 2 * p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      unsigned long long w1 =
+          __hip_atomic_load(slots + 2 * p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       unsigned spins = 0;
-      while (b == 0ull) {
+      while ((w0 ^ w1) != tag) {
         if (++spins > kSpinLimit) {  // never expected: report and give up
           __hip_atomic_fetch_add(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          b = Slot<Acc>::enc((Acc)0);
+          w0 = key.m0;  // reads as 0
           break;
         }
         __builtin_amdgcn_s_sleep(1);
-        b = __hip_atomic_load(slots + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        w0 = __hip_atomic_load(slots + 2 * p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        w1 = __hip_atomic_load(slots + 2 * p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-      v = Slot<Acc>::dec(b);
+      v = from_bits64<Acc>(w0 ^ key.m0);
     }
     carry += wave_total(v);
   }
@@ -279,8 +277,8 @@ __device__ Acc carry_in(const unsigned long long* __restrict__ slots, int chunk,
 template <typename In, typename Out, typename Acc, bool REV, bool VEC>
 __global__ __launch_bounds__(kThreads, 4) void scan_rows_kernel(
     const In* __restrict__ x, Out* __restrict__ y, int64_t D, int nchunk, int tiles,
-    int64_t total_chunks, unsigned long long* __restrict__ slots,
-    unsigned* __restrict__ row_done, unsigned* __restrict__ err) {
+    int64_t total_chunks, unsigned long long* __restrict__ slots, SlotKey key,
+    unsigned* __restrict__ err) {
   __shared__ Acc s_wave[2][4];
   __shared__ Acc s_carry;
   const int lane = threadIdx.x & 63;
@@ -321,28 +319,12 @@ __global__ __launch_bounds__(kThreads, 4) void scan_rows_kernel(
     }
 
     Acc carry = (Acc)0;
-    unsigned prev_done = 0;  // the row's completion count before this chunk's
     if (nchunk > 1) {
-      unsigned long long* row_slots = slots + row * nchunk;
+      unsigned long long* row_slots = slots + 2 * row * nchunk;
       if (wave == 0) {
-        if (lane == 0 && chunk + 1 < nchunk)
-          __hip_atomic_store(row_slots + chunk, Slot<Acc>::enc(chunk_total), __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-        const Acc c = carry_in<Acc>(row_slots, chunk, lane, err);
+        if (lane == 0 && chunk + 1 < nchunk) publish<Acc>(row_slots, chunk, chunk_total, key);
+        const Acc c = carry_in<Acc>(row_slots, chunk, lane, key, err);
         if (lane == 0) s_carry = c;
-        // This chunk has read its carry and counts itself done; the last
-        // chunk of the row to do so zeroes the row's slots after its output
-        // (below).  The publish must be visible before the count: wait for
-        // its acknowledgement (vmcnt counts stores in issue order, so for
-        // chunk > 0 the carry loads above already waited for it).  The
-        // count's result is used only by lane 0, after the output stores are
-        // issued (the library is built without the AMDGPU atomic optimizer,
-        // which would broadcast the result to the wave, and wait for it,
-        // right here).
-        __builtin_amdgcn_s_waitcnt(0x0F70);
-        if (lane == 0)
-          prev_done = __hip_atomic_fetch_add(row_done + row, 1u, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT);
       }
       __syncthreads();
       carry = s_carry;
@@ -366,14 +348,6 @@ __global__ __launch_bounds__(kThreads, 4) void scan_rows_kernel(
         emit_tile<In, Out, Acc, REV, VEC>(s, run + wave_off, yr, D, c0 + tt * kTile + lane_off);
         run += (s_wave[phase][0] + s_wave[phase][1]) + (s_wave[phase][2] + s_wave[phase][3]);
       }
-    }
-    if (nchunk > 1 && wave == 0 && lane == 0 && prev_done == (unsigned)nchunk - 1) {
-      // Every chunk of the row has read its carry: zero the row's slots (and
-      // the counter) for the next call.
-      unsigned long long* row_slots = slots + row * nchunk;
-      for (int p = 0; p < nchunk - 1; ++p)
-        __hip_atomic_store(row_slots + p, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(row_done + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     phase ^= 1;
     // s_carry and the other s_wave buffer are rewritten only after the next
@@ -399,9 +373,27 @@ Plan plan(int64_t rows, int64_t D) {
   return p;
 }
 
-size_t workspace_bytes(const Plan& p, int64_t rows) {
-  // slots, one 4-byte counter per row, one 8-byte word (hang-guard counter)
-  return p.slots > 0 ? (size_t)p.slots * 8 + (size_t)nl2k::ceil_div(rows, 2) * 8 + 8 : 0;
+size_t workspace_bytes(const Plan& p) {
+  // a two-word slot per chunk, then one 8-byte word (hang-guard counter)
+  return p.slots > 0 ? (size_t)p.slots * 16 + 8 : 0;
+}
+
+// A fresh nonce per call (process-wide, never 0; seeded from the clock so a
+// reloaded library does not repeat an earlier run's nonces) and its masks.
+unsigned long long splitmix64(unsigned long long z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+SlotKey next_key() {
+  static std::atomic<unsigned long long> counter{
+      splitmix64((unsigned long long)std::chrono::steady_clock::now().time_since_epoch().count())};
+  unsigned long long n = counter.fetch_add(1, std::memory_order_relaxed);
+  if (n == 0) n = counter.fetch_add(1, std::memory_order_relaxed);
+  const unsigned long long m0 = splitmix64(n ^ 0xD1B54A32D192ED03ull);
+  return SlotKey{m0, m0 ^ n};
 }
 
 int validate(int64_t rows, int64_t D, const char* who) {
@@ -423,18 +415,18 @@ int run(const In* x, Out* y, int64_t rows, int64_t D, void* workspace, size_t ws
   if (!x || !y) return nl2k::fail(NL2K_ERR_NULL, "%s: null pointer argument", who);
   const Plan p = plan(rows, D);
   unsigned long long* slots = nullptr;
-  unsigned* row_done = nullptr;
   unsigned* err = nullptr;
+  SlotKey key{0, 0};
   if (p.slots > 0) {
-    const size_t need = workspace_bytes(p, rows);
+    const size_t need = workspace_bytes(p);
     if (!workspace || ws_bytes < need)
       return nl2k::fail(NL2K_ERR_WORKSPACE, "%s: workspace of %zu bytes required, got %zu", who,
                         need, workspace ? ws_bytes : (size_t)0);
     if ((reinterpret_cast<uintptr_t>(workspace) & 7u) != 0)
       return nl2k::fail(NL2K_ERR_ALIGN, "%s: workspace must be 8-byte aligned", who);
     slots = static_cast<unsigned long long*>(workspace);
-    row_done = reinterpret_cast<unsigned*>(slots + p.slots);
-    err = row_done + nl2k::ceil_div(rows, 2) * 2;
+    err = reinterpret_cast<unsigned*>(slots + 2 * p.slots);
+    key = next_key();
   }
   const bool vec = D % 4 == 0 && nl2k::aligned16(x) && nl2k::aligned16(y);
   // Single-chunk rows never wait, so their grid is not capped.
@@ -443,11 +435,11 @@ int run(const In* x, Out* y, int64_t rows, int64_t D, void* workspace, size_t ws
   if (vec)
     hipLaunchKernelGGL((scan_rows_kernel<In, Out, Acc, REV, true>), dim3((unsigned)grid),
                        dim3(kThreads), 0, stream, x, y, D, p.nchunk, p.tiles, p.total, slots,
-                       row_done, err);
+                       key, err);
   else
     hipLaunchKernelGGL((scan_rows_kernel<In, Out, Acc, REV, false>), dim3((unsigned)grid),
                        dim3(kThreads), 0, stream, x, y, D, p.nchunk, p.tiles, p.total, slots,
-                       row_done, err);
+                       key, err);
   return nl2k::check_launch(who);
 }
 
@@ -459,7 +451,7 @@ const char* scan_last_error(void) { return nl2k::error_slot().text; }
 
 size_t scan_workspace_bytes(int64_t rows, int64_t D) {
   if (validate(rows, D, "scan_workspace_bytes")) return 0;
-  return workspace_bytes(plan(rows, D), rows);
+  return workspace_bytes(plan(rows, D));
 }
 
 int scan_forward_f32(const float* x, float* y, int64_t rows, int64_t D, void* workspace,

@@ -53,13 +53,12 @@ _WORKSPACES = {}
 
 
 def _workspace(device, stream, nbytes):
-    """The zero-initialised workspace kept for (device, stream): the kernels
-    leave it zeroed after every call, so it is allocated (and zeroed) only
-    when a larger one is needed."""
+    """The workspace kept for (device, stream), allocated only when a larger
+    one is needed (the kernels need no initial contents)."""
     key = (device.index, stream.value)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() * 8 < nbytes:
-        ws = torch.zeros(max((nbytes + 7) // 8, 1), dtype=torch.int64, device=device)
+        ws = torch.empty(max((nbytes + 7) // 8, 1), dtype=torch.int64, device=device)
         _WORKSPACES[key] = ws
     return ws
 

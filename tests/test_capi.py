@@ -116,12 +116,11 @@ def test_scan_argument_validation_and_plan_without_gpu():
     st = lib.scan_forward_f32(None, fake, 4, 16, None, 0, None)
     assert st == STATUS["NL2K_ERR_NULL"]
     # rows of one 4096-element chunk need no workspace; longer rows need one
-    # 8-byte slot per chunk, a 4-byte counter per row (rounded to 8 bytes)
-    # and one word
+    # two-word (16-byte) slot per chunk and one word
     assert lib.scan_workspace_bytes(4096, 4096) == 0
-    assert lib.scan_workspace_bytes(64, 65536) == 64 * 16 * 8 + 32 * 8 + 8
+    assert lib.scan_workspace_bytes(64, 65536) == 64 * 16 * 16 + 8
     # 2^21 + 5 elements: 513 tiles -> 171 chunks of 3
-    assert lib.scan_workspace_bytes(2, 2**21 + 5) == 2 * 171 * 8 + 8 + 8
+    assert lib.scan_workspace_bytes(2, 2**21 + 5) == 2 * 171 * 16 + 8
     need = lib.scan_workspace_bytes(64, 65536)
     st = lib.scan_forward_f32(fake, fake, 64, 65536, fake, need - 8, None)
     assert st == STATUS["NL2K_ERR_WORKSPACE"]

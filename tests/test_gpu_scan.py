@@ -129,7 +129,9 @@ def test_scan_rejects_bad_arguments():
 def test_scan_full_size_identities():
     """At the acceptance size: the last column equals the float64 row sums,
     the reverse scan equals flip(scan(flip)) bit for bit, repeated calls are
-    bitwise identical, and the C-ABI's hang-guard counter stays zero."""
+    bitwise identical, a workspace needs no initial contents (zeros, random
+    bits, and what the previous call left all give the same results), and
+    the C-ABI's hang-guard counter stays zero."""
     announce("scan identities [64, 65536]")
     op = _op()
     lib = op._lib()
@@ -144,19 +146,23 @@ def test_scan_full_size_identities():
     rowsum = x.double().sum(dim=1).float()
     assert torch.allclose(y1[:, -1], rowsum, atol=1e-3, rtol=1e-3)
     assert torch.allclose(rb[:, 0], rowsum, atol=1e-3, rtol=1e-3)
-    # direct C-ABI calls on a fresh zeroed workspace: every call leaves it
-    # zeroed again (slots and per-row counters; the last word counts
-    # hang-guard trips, which must stay 0)
+    # direct C-ABI calls on one workspace, first zero-filled, then random
+    # bits (all but the last word, which counts hang-guard trips and must
+    # stay 0), then reused as the previous calls left it
     rows, d = x.shape
     nbytes = lib.scan_workspace_bytes(rows, d)
     ws = torch.zeros(nbytes // 8, dtype=torch.int64, device="cuda")
-    for fn in (lib.scan_forward_f32, lib.scan_backward_f32, lib.scan_forward_f32):
+    junk = torch.randint(-2**62, 2**62, (nbytes // 8 - 1,), generator=torch.Generator().manual_seed(5))
+    for k, fn in enumerate((lib.scan_forward_f32, lib.scan_backward_f32, lib.scan_forward_f32,
+                            lib.scan_forward_f32)):
+        if k == 1:
+            ws[:-1].copy_(junk.cuda())
         y3 = torch.empty_like(x)
         st = fn(capi.ptr(x), capi.ptr(y3), rows, d, capi.ptr(ws), nbytes, capi.stream_of(x))
         assert st == 0, lib.scan_last_error()
         torch.cuda.synchronize()
         assert torch.equal(y3, y1 if fn is lib.scan_forward_f32 else rb)
-        assert int(torch.count_nonzero(ws)) == 0, "workspace not left zeroed"
+        assert int(ws[-1]) == 0, "hang guard tripped"
 
 
 def test_scan_verify_all_reference_defaults():
