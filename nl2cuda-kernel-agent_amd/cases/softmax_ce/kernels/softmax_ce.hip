@@ -26,8 +26,9 @@
 //    like the forward so each row's lse and label are read once.
 //  * A label outside [0, C) makes its row's loss term and gradient NaN (the
 //    reference would index out of the row; torch raises).
-//  * C not a multiple of 4, misaligned rows or C > 8192 use a generic
-//    workgroup-per-row kernel (three passes over the row from L2).
+//  * C not a multiple of 4, misaligned rows or C > 8192 use generic kernels:
+//    a workgroup per row for the forward (two passes over the row, the
+//    second from L2) and a flat grid-stride backward.
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
@@ -175,7 +176,7 @@ __global__ __launch_bounds__(kBlock) void sce_fwd_kernel(
 }
 
 // Generic forward (any C and alignment): workgroups stride over the rows,
-// one row at a time, three passes over it (max, sum of exp) from L2.
+// one row at a time, two passes over it (max, then the sum of exp).
 __global__ __launch_bounds__(kBlock) void sce_fwd_generic_kernel(
     const float* __restrict__ logits, const int64_t* __restrict__ labels,
     float* __restrict__ lse_out, float* __restrict__ partial, int64_t B, int64_t C) {
