@@ -545,6 +545,334 @@ __global__ __launch_bounds__(512) void pair_bwd_d64_kernel(
 // Region plan and workspace layout (floats): partial (W.Y) [nRJ][N][64],
 // partial row sums [nRJ][N] (sums only), partial (W^T.X) [nRI][M][64],
 // partial column sums [nRI][M] (sums only).
+// ------------------------------------------------- backward, three roles
+// The same region walk, staging pipeline, operand layouts and partial
+// outputs as pair_bwd_d64_kernel, by workgroups of twelve waves in three
+// roles, one wave of each per SIMD (wave w on SIMD w % 4):
+//  * waves 0-3 run only the (W.Y)^T contraction (rows 16 (w & 3)..) and
+//    flush its partials per i-chunk;
+//  * waves 4-7 run only the (W^T.X)^T contraction (columns 16 (w & 3)..)
+//    and flush at the end;
+//  * waves 8-11 stage, as waves 4-7 do there, with one X register stage
+//    loaded one step ahead (issued first in its step, so waiting for it
+//    retires only loads at least two steps old apart from itself).
+// Each SIMD thus has two waves issuing MFMAs, and one's waits on LDS,
+// barriers or its partial stores are covered by the other's matrix work;
+// every accumulator sees the same MFMA sequence, so the partials are
+// bit-identical to pair_bwd_d64_kernel's.  The role index is read through
+// readfirstlane so the compiler sees wave-uniform branches and gives each
+// role its own live ranges (168 VGPRs, three waves per SIMD).
+template <class Op, int JC, bool kVecNM>
+__global__ __launch_bounds__(768) void pair_bwd_d64_3r_kernel(
+    const float* __restrict__ X, const float* __restrict__ Y,
+    const float* dK, const float* Kf,
+    float* __restrict__ Px, float* __restrict__ Rx, float* __restrict__ Py,
+    float* __restrict__ Ry, int N, int M, int RI, int nRJ,
+    const float* __restrict__ sx, const float* __restrict__ sy) {
+  // dK and Kf are deliberately not __restrict__: with it the compiler treats
+  // their loads as invariant and sinks the prefetch of tile t+2 past the
+  // workgroup barriers to its use, which serialises the memory latency.
+  constexpr int RJ = JC * kTile;
+  constexpr int kYtLds = RJ + 4;
+  __shared__ __attribute__((aligned(16))) float P[2][kTileFloats];
+  __shared__ __attribute__((aligned(16))) float Xt[2][kTileFloats];
+  __shared__ __attribute__((aligned(16))) float Yt[kD * kYtLds];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform role
+  const int n = lane & 15;
+  const int h = lane >> 4;
+
+  const int ri = blockIdx.x / nRJ;
+  const int rj = blockIdx.x - ri * nRJ;
+  const int ibase = ri * RI;
+  const int jbase = rj * RJ;
+  const int rows = min(RI, N - ibase);
+  const int cols = min(RJ, M - jbase);
+  const int n_ic = (rows + kTile - 1) / kTile;
+  const int n_jc = (cols + kTile - 1) / kTile;
+  const int n_tiles = n_ic * n_jc;
+
+  // Staging-wave state (declared for all waves; only waves 8-11 use it).
+  const int ptid = tid - 512;
+  // W: float4 (row (p>>4) + 16 s, cols 4 (p & 15)..), s = 0..3.
+  const int srow = (ptid >> 4) & 15;
+  const int scol = (ptid & 15) * 4;
+  // X chunk: row p & 63 (lanes along rows), float4 columns (p>>6) + 4 s.
+  const int xrow = ptid & 63;
+  const int xcol = ((ptid >> 6) & 3) * 4;
+  f32x4 g_dk[3][4], g_k[3][4], g_x[4];
+  float g_xs;
+  bool g_ok[3][4];
+  auto load_stage = [&](int t, f32x4 (&dk)[4], f32x4 (&kk)[4], bool (&ok)[4]) {
+    const int ic = t / n_jc, jc = t - ic * n_jc;
+    const int ib = ibase + ic * kTile;
+    const int jb = jbase + jc * kTile;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int gi = ib + srow + 16 * s;
+      const int gj = jb + scol;
+      const int ci = min(gi, N - 1);
+      if (kVecNM) {
+        ok[s] = gi < N && gj < M;
+        const size_t o = (size_t)ci * M + min(gj, M - 4);
+        dk[s] = load4(dK + o);
+        if constexpr (Op::kProduct) kk[s] = load4(Kf + o);
+      } else {
+        ok[s] = gi < N;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const size_t o = (size_t)ci * M + min(gj + u, M - 1);
+          const bool in = gj + u < M;
+          const float a = dK[o];
+          dk[s][u] = in ? a : 0.f;
+          if constexpr (Op::kProduct) {
+            const float b = Kf[o];
+            kk[s][u] = in ? b : 0.f;
+          }
+        }
+      }
+    }
+  };
+  auto commit_stage = [&](int t, const f32x4 (&dk)[4], const f32x4 (&kk)[4],
+                          const bool (&ok)[4]) {
+    float* dst = P[t & 1];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      if constexpr (Op::kProduct)
+        store4(&dst[(srow + 16 * s) * kLds + scol], ok[s] ? dk[s] * kk[s] : zero4());
+      else
+        store4(&dst[(srow + 16 * s) * kLds + scol], ok[s] ? dk[s] : zero4());
+    }
+  };
+  auto load_x = [&](int ic, f32x4 (&xs)[4], float& sc) {
+    const size_t r = (size_t)min(ibase + ic * kTile + xrow, N - 1);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) xs[s] = load4(X + r * kD + xcol + 16 * s);
+    if constexpr (Op::kScale) sc = sx[r];
+  };
+  auto commit_x = [&](int ic, const f32x4 (&xs)[4], float sc) {
+    float* dst = Xt[ic & 1];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if constexpr (Op::kScale)
+          dst[(xcol + 16 * s + u) * kLds + xrow] = xs[s][u] * sc;
+        else
+          dst[(xcol + 16 * s + u) * kLds + xrow] = xs[s][u];
+      }
+  };
+  // X chunk published at step t: the one after the chunk of tile t (clamped;
+  // at the last chunk that rewrites the chunk in use with identical bits).
+  auto x_chunk = [&](int t) { return min(t / n_jc + 1, n_ic - 1); };
+
+  // Tile 0's loads go out first, then waves 0-7 stage the region's Y rows
+  // (Yt <- Y[jbase .. jbase+RJ), transposed, lanes along j so the transposed
+  // LDS writes hit consecutive banks) while they are in flight.
+  if (wave >= 8) {
+    load_x(0, g_x, g_xs);
+    load_stage(0, g_dk[0], g_k[0], g_ok[0]);
+  }
+  constexpr int kYtPerThread = RJ * 16 / 512;
+  f32x4 yv[kYtPerThread];
+  float ys[kYtPerThread];
+  if (tid < 512) {
+#pragma unroll
+    for (int k = 0; k < kYtPerThread; ++k) {
+      const int f = tid + 512 * k;
+      const size_t yr = (size_t)min(jbase + f % RJ, M - 1);
+      yv[k] = load4(Y + yr * kD + (f / RJ) * 4);
+      if constexpr (Op::kScale) ys[k] = sy[yr];
+    }
+#pragma unroll
+    for (int k = 0; k < kYtPerThread; ++k) {
+      const int f = tid + 512 * k;
+      const int j = f % RJ;
+      const int c = (f / RJ) * 4;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if constexpr (Op::kScale)
+          Yt[(c + u) * kYtLds + j] = yv[k][u] * ys[k];
+        else
+          Yt[(c + u) * kYtLds + j] = yv[k][u];
+      }
+    }
+  }
+  // Both roles pass 1 + n_steps barriers; the staging loop is unrolled by
+  // three, so the compute side pads its tile barriers up to n_steps.
+  const int n_steps = (n_tiles + 2) / 3 * 3;
+
+  if (wave >= 8) {
+    // ------------------------------------------------------ staging waves
+    // Every step t runs the same straight-line sequence (no branches, so the
+    // loads of later tiles stay in flight across steps): publish the X chunk
+    // after tile t's (its registers were loaded last step), load the X chunk
+    // for step t+1, load tile t+3 into the register stage published last
+    // step, then publish W of tile t+1 from stage (t+1) % 3, loaded two steps
+    // ago.  The memory counter retires in order, so the X wait, on the
+    // step's oldest young load, retires nothing younger than two steps but
+    // that load.  Indices are clamped: loads past the last tile fetch valid
+    // data nobody uses; commits past it fill the idle P buffer.  A
+    // republished X chunk rewrites the buffer the compute waves are reading
+    // only with identical bits.  The three W register stages are addressed
+    // statically (the loop is unrolled by three): a runtime stage index would
+    // be if-converted into selects on the loaded data, forcing a wait right
+    // after each load.
+    commit_x(0, g_x, g_xs);
+    load_x(x_chunk(0), g_x, g_xs);
+    load_stage(min(1, n_tiles - 1), g_dk[1], g_k[1], g_ok[1]);
+    load_stage(min(2, n_tiles - 1), g_dk[2], g_k[2], g_ok[2]);
+    commit_stage(0, g_dk[0], g_k[0], g_ok[0]);
+    __syncthreads();
+    auto step = [&](int t, f32x4 (&ldk)[4], f32x4 (&lk)[4], bool (&lok)[4],
+                    const f32x4 (&cdk)[4], const f32x4 (&ck)[4], const bool (&cok)[4]) {
+      __builtin_amdgcn_sched_barrier(0);
+      commit_x(x_chunk(t), g_x, g_xs);
+      load_x(x_chunk(t + 1), g_x, g_xs);
+      load_stage(min(t + 3, n_tiles - 1), ldk, lk, lok);
+      commit_stage(t + 1, cdk, ck, cok);
+      __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();
+    };
+    for (int t = 0; t < n_steps; t += 3) {
+      step(t, g_dk[0], g_k[0], g_ok[0], g_dk[1], g_k[1], g_ok[1]);
+      step(t + 1, g_dk[1], g_k[1], g_ok[1], g_dk[2], g_k[2], g_ok[2]);
+      step(t + 2, g_dk[2], g_k[2], g_ok[2], g_dk[0], g_k[0], g_ok[0]);
+    }
+    return;
+  }
+
+  // ------------------------------------------------------- compute waves
+  const int wb = wave & 3;  // 16-row block of (W.Y)^T / 16-column block of (W^T.X)^T
+  __syncthreads();
+  if (wave < 4) {
+    // (W.Y)^T rows 16 wb.. of every tile, accumulated over the region's
+    // columns and flushed per i-chunk (dX side).
+    for (int ic = 0; ic < n_ic; ++ic) {
+      f32x4 accX[4];
+#pragma unroll
+      for (int db = 0; db < 4; ++db) accX[db] = zero4();
+      float rp = 0.f;
+#pragma unroll
+      for (int jc = 0; jc < JC; ++jc) {
+        if (jc < n_jc) {
+          const int t = ic * n_jc + jc;
+          const float* Pb = P[t & 1];
+          const float* Yb = Yt + jc * kTile;
+          f32x4 xa[2], xbv[2][4];
+          xa[0] = load4(&Pb[(wb * 16 + n) * kLds + 4 * h]);
+#pragma unroll
+          for (int db = 0; db < 4; ++db) xbv[0][db] = load4(&Yb[(db * 16 + n) * kYtLds + 4 * h]);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int c = q & 1;
+            if (q < 3) {
+              const int k1 = 16 * (q + 1) + 4 * h;
+              xa[c ^ 1] = load4(&Pb[(wb * 16 + n) * kLds + k1]);
+#pragma unroll
+              for (int db = 0; db < 4; ++db) xbv[c ^ 1][db] = load4(&Yb[(db * 16 + n) * kYtLds + k1]);
+            }
+            if constexpr (Op::kSums) rp += (xa[c][0] + xa[c][1]) + (xa[c][2] + xa[c][3]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+              for (int db = 0; db < 4; ++db) accX[db] = mfma16x4(xa[c][u], xbv[c][db][u], accX[db]);
+          }
+          __syncthreads();
+        }
+      }
+      const size_t slot = (size_t)rj * N;
+      const int i_base = ibase + ic * kTile + wb * 16;
+      if constexpr (Op::kSums) {
+        float rs = rp;
+        rs += __shfl_xor(rs, 16, 64);
+        rs += __shfl_xor(rs, 32, 64);
+        if (h == 0 && i_base + n < N) Rx[slot + i_base + n] = rs;
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = i_base + 4 * h + r;
+        if (i < N) {
+#pragma unroll
+          for (int db = 0; db < 4; ++db) Px[(slot + i) * kD + db * 16 + n] = accX[db][r];
+        }
+      }
+    }
+    for (int t = n_tiles; t < n_steps; ++t) __syncthreads();
+    return;
+  }
+
+  // (W^T.X)^T columns 16 wb.. of every tile, accumulated over the region's
+  // rows (dY side), flushed at the end.
+  f32x4 accY[JC][4];
+  float cp[JC];
+#pragma unroll
+  for (int c = 0; c < JC; ++c) {
+    cp[c] = 0.f;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) accY[c][db] = zero4();
+  }
+  for (int ic = 0; ic < n_ic; ++ic) {
+    const float* Xb = Xt[ic & 1];
+#pragma unroll
+    for (int jc = 0; jc < JC; ++jc) {
+      if (jc < n_jc) {
+        const int t = ic * n_jc + jc;
+        const float* Pb = P[t & 1];
+        f32x4 yb[2][4];
+        float ya[2][4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) ya[0][u] = Pb[(4 * h + u) * kLds + wb * 16 + n];
+#pragma unroll
+        for (int db = 0; db < 4; ++db) yb[0][db] = load4(&Xb[(db * 16 + n) * kLds + 4 * h]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int c = q & 1;
+          if (q < 3) {
+            const int k1 = 16 * (q + 1) + 4 * h;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) ya[c ^ 1][u] = Pb[(k1 + u) * kLds + wb * 16 + n];
+#pragma unroll
+            for (int db = 0; db < 4; ++db) yb[c ^ 1][db] = load4(&Xb[(db * 16 + n) * kLds + k1]);
+          }
+          if constexpr (Op::kSums) cp[jc] += (ya[c][0] + ya[c][1]) + (ya[c][2] + ya[c][3]);
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+              accY[jc][db] = mfma16x4(ya[c][u], yb[c][db][u], accY[jc][db]);
+        }
+        __syncthreads();
+      }
+    }
+  }
+  for (int t = n_tiles; t < n_steps; ++t) __syncthreads();
+
+  const size_t slot = (size_t)ri * M;
+#pragma unroll
+  for (int jc = 0; jc < JC; ++jc) {
+    if (jc < n_jc) {
+      const int j_base = jbase + jc * kTile + wb * 16;
+      if constexpr (Op::kSums) {
+        float cs = cp[jc];
+        cs += __shfl_xor(cs, 16, 64);
+        cs += __shfl_xor(cs, 32, 64);
+        if (h == 0 && j_base + n < M) Ry[slot + j_base + n] = cs;
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = j_base + 4 * h + r;
+        if (j < M) {
+#pragma unroll
+          for (int db = 0; db < 4; ++db) Py[(slot + j) * kD + db * 16 + n] = accY[jc][db][r];
+        }
+      }
+    }
+  }
+}
+
 struct BwdPlan {
   bool fast = false;
   int R = 64;  // region edge (rows and columns)
@@ -587,9 +915,12 @@ void launch_bwd_tiles(const BwdPlan& p, const float* X, const float* Y, const fl
   float* Rx = ws + p.rx;
   float* Py = ws + p.py;
   float* Ry = ws + p.ry;
+  // Vector loads of the upstream tiles: the three-role kernel.  Scalar
+  // loads (M % 4 != 0 or misaligned): the eight-wave kernel, which measured
+  // faster there (its staging needs the registers the third role takes).
   if (vec_nm)
-    hipLaunchKernelGGL((pair_bwd_d64_kernel<Op, JC, true>), dim3(p.nRI * p.nRJ), dim3(512), 0,
-                       stream, X, Y, dK, K, Px, Rx, Py, Ry, N, M, p.R, p.nRJ, sx, sy);
+    hipLaunchKernelGGL((pair_bwd_d64_3r_kernel<Op, JC, true>), dim3(p.nRI * p.nRJ), dim3(768),
+                       0, stream, X, Y, dK, K, Px, Rx, Py, Ry, N, M, p.R, p.nRJ, sx, sy);
   else
     hipLaunchKernelGGL((pair_bwd_d64_kernel<Op, JC, false>), dim3(p.nRI * p.nRJ), dim3(512), 0,
                        stream, X, Y, dK, K, Px, Rx, Py, Ry, N, M, p.R, p.nRJ, sx, sy);
