@@ -244,7 +244,7 @@ def main():
         "bwd_tflops": round(bwd_tf, 2),
         "pct_fp32_roofline": round(100 * (ff + bf) / (step_ms * 1e-3) / 1e12 / FP32_PEAK_TFLOPS, 2),
         "roofline": {
-            "kernel": "rbf_backward_f32 (pair_bwd_d64_kernel<RbfBwdOp> + rbf_bwd_reduce_kernel)",
+            "kernel": "rbf_backward_f32 (pair_bwd_d64_3r_kernel<RbfBwdOp> + rbf_bwd_reduce_kernel)",
             "bound": "mfma",
             "achieved": round(bwd_tf, 3),
             "peak": FP32_PEAK_TFLOPS,
