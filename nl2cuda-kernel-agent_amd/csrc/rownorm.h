@@ -20,8 +20,9 @@
 //    own a row (TPR = 64: one wave per row, TPR = 256: one workgroup per
 //    row), each thread keeps V float4 of the row in registers, so the row is
 //    read from HBM exactly once.  Statistics are exact two-pass sums over the
-//    registers; reductions are wave64 butterflies (DPP / ds_swizzle via
-//    __shfl_xor) plus one LDS step across waves.
+//    registers; reductions are wave64 DPP lane moves (quad_perm and row
+//    mirrors within each 16-lane row, then v_readlane across the four rows)
+//    plus one LDS step across waves.
 //  * Backward: a workgroup walks a contiguous block of rows, prefetching the
 //    next row's dy and x while it finishes the current one, and accumulates
 //    its partial dw (/ dbias) in registers.  The per-block partials ([G][D])
@@ -56,8 +57,8 @@ __device__ __forceinline__ float hsum4(f32x4 a) { return (a[0] + a[1]) + (a[2] +
 // of them.  `red` is a per-block LDS scratch of at least 2 * 4 floats.
 template <int TPR>
 __device__ __forceinline__ void row_sum2(float& a, float& b, float* red) {
-  a = wave_sum(a);
-  b = wave_sum(b);
+  a = wave_sum_dpp(a);
+  b = wave_sum_dpp(b);
   if (TPR == 256) {
     const int wave = threadIdx.x >> 6;
     __syncthreads();  // red may still be read from the previous use
