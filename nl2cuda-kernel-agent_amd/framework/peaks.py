@@ -20,7 +20,17 @@ last-level cache (MALL), so the rates are HBM rates.
 Each rate is the median of --iters launches timed with HIP events on the
 launch stream.  Prints one JSON line per rate and a table.
 
+--sized-copy MiB[,MiB...] instead measures the copy kernel at the sizes of
+the streaming cases (for example 16 MiB in + 16 MiB out is a [64, 65536]
+fp32 scan), with a 512 MiB read between launches so that neither buffer
+starts in the MALL, over the same sweep of workgroup counts.  At these
+sizes the launch ramp and the tail are a visible share of the time, so the
+copy rate there is the practical ceiling of a kernel that reads and writes
+that many bytes once.  Run it under rocprofv3 --kernel-trace --stats for the
+kernel-time figures beside the event times printed here.
+
 Usage:  python nl2cuda-kernel-agent_amd/framework/peaks.py [--iters 20]
+        python nl2cuda-kernel-agent_amd/framework/peaks.py --sized-copy 16,64,128
 """
 
 import argparse
@@ -79,15 +89,84 @@ def _median_ms(fn, iters, stream):
     return statistics.median(ts)
 
 
+def _median_ms_flushed(fn, flush, iters, stream):
+    """Like _median_ms, with flush() run (outside the timed region) before
+    every launch."""
+    import torch
+    ts = []
+    for i in range(iters + 3):
+        flush()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        if i >= 3:
+            ts.append(e0.elapsed_time(e1))
+    return statistics.median(ts)
+
+
+def sized_copy(sizes_mib, iters, blocks=None):
+    """Copy kernel at the given sizes, with a 512 MiB read flush before each
+    launch; prints one JSON line per launch shape and the best per size."""
+    import torch
+    dev = torch.device("cuda:0")
+    lib = _lib()
+    stream = torch.cuda.current_stream(dev)
+    s = capi.stream_of(torch.empty(1, device=dev))
+    P = capi.ptr
+
+    def ok(st):
+        capi.check(st, lib.peaks_last_error, "peaks")
+
+    fl_n4 = (512 << 20) // 16
+    fl = torch.ones(fl_n4 * 4, device=dev)
+    sink = torch.empty(max(SWEEP_BLOCKS), device=dev)
+
+    def flush():
+        ok(lib.peaks_read_f32x4(P(fl), fl_n4, P(sink), 8192, 8, s))
+
+    rows = []
+    for mib in sizes_mib:
+        n4 = (mib << 20) // 16
+        a = torch.ones(n4 * 4, device=dev)
+        b = torch.empty_like(a)
+        top = None
+        for g in blocks or (256, 512) + SWEEP_BLOCKS:
+            t = _median_ms_flushed(lambda g=g: ok(lib.peaks_copy_f32x4(P(a), P(b), n4, g, s)),
+                                   flush, iters, stream)
+            gbs = 2 * (mib << 20) / (t * 1e-3) / 1e9
+            print(json.dumps({"rate": f"copy {mib} MiB", "launch": f"{g} x 256",
+                              "gbs": round(gbs, 1), "ms": round(t, 4)}), flush=True)
+            if top is None or gbs > top[0]:
+                top = (gbs, t, g)
+        rows.append((mib, top))
+        del a, b
+    print("\n| bytes in + out | best launch | event time | rate (in + out) | fraction of 8 TB/s |")
+    print("|---|---|---:|---:|---:|")
+    for mib, (gbs, t, g) in rows:
+        print(f"| {mib} + {mib} MiB | {g} x 256 | {1000 * t:.2f} µs | {gbs:,.0f} GB/s | "
+              f"{100 * gbs / HBM_PEAK_GBS:.1f} % |")
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--mfma-iters", type=int, default=4000, help="even")
+    ap.add_argument("--sized-copy", default=None,
+                    help="comma-separated MiB: copy at these sizes (flushed) instead")
+    ap.add_argument("--blocks", default=None,
+                    help="comma-separated workgroup counts for --sized-copy (default: a sweep)")
     ns = ap.parse_args(argv)
     import torch
     if not torch.cuda.is_available():
         print("peaks: needs the GPU", file=sys.stderr)
         return 2
+    if ns.sized_copy:
+        blocks = tuple(int(v) for v in ns.blocks.split(",")) if ns.blocks else None
+        return sized_copy([int(v) for v in ns.sized_copy.split(",")], ns.iters, blocks)
     dev = torch.device("cuda:0")
     lib = _lib()
     stream = torch.cuda.current_stream(dev)
