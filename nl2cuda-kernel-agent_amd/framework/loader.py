@@ -96,6 +96,8 @@ def build_library(name, sources, base_dir=None, extra_cuda_cflags=None,
         print(" ".join(cmd), file=sys.stderr)
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
+        if os.path.exists(tmp):
+            os.remove(tmp)
         raise RuntimeError(f"hipcc failed for lib{name}.so:\n{proc.stderr[-4000:]}")
     os.replace(tmp, out)
     with open(out + ".stamp", "w") as f:

@@ -56,8 +56,9 @@ def compare_tensors(got, ref, atol=None, rtol=None):
     if g.numel() == 0:
         return True, 0.0, 0.0
     diff = (g - r).abs()
-    ok = bool(torch.all(diff <= atol + rtol * r.abs()).item()) and \
-        bool(torch.equal(torch.isnan(g), torch.isnan(r)))
+    # torch.allclose's rule (the reference's check): |g - r| <= atol + rtol |r|,
+    # equal infinities close, NaN never close.
+    ok = bool(torch.isclose(g, r, rtol=rtol, atol=atol).all().item())
     max_abs = torch.nan_to_num(diff, nan=0.0).max().item()
     rel = diff / r.abs().clamp_min(1e-30)
     max_rel = torch.nan_to_num(rel, nan=0.0, posinf=0.0).max().item()

@@ -1,0 +1,74 @@
+"""The parity harness on the CPU (framework/verify.py): the comparison rule
+is torch.allclose's at atol = rtol = 1e-3 (the reference's check,
+framework/verify.py:35-105), integers compare exactly, and verify_all reports
+PASS for the reference itself and FAIL for a forward or a gradient with a
+planted mistake."""
+
+import torch
+
+from framework.verify import compare_tensors, verify_all
+
+INF, NAN = float("inf"), float("nan")
+
+
+def test_compare_follows_allclose():
+    ref = torch.tensor([1.0, -2.0, 0.0, INF, -INF])
+    ok, a, r = compare_tensors(ref + torch.tensor([9e-4, -2e-3, 9.9e-4, 0.0, 0.0]), ref)
+    assert ok  # within atol + rtol |ref| everywhere; equal infinities are close
+    assert abs(a - 2e-3) < 1e-6 and r > 0
+    assert not compare_tensors(torch.tensor([1.0021]), torch.tensor([1.0]))[0]
+    assert not compare_tensors(torch.tensor([INF]), torch.tensor([-INF]))[0]
+    assert not compare_tensors(torch.tensor([NAN]), torch.tensor([NAN]))[0]
+    assert not compare_tensors(torch.tensor([1.0]), torch.tensor([NAN]))[0]
+    for t in (ref, torch.tensor([1.0, 2.0])):
+        assert torch.allclose(t, t) == compare_tensors(t, t)[0]
+
+
+def test_compare_integers_and_shapes():
+    x = torch.tensor([1, -5, 7], dtype=torch.int32)
+    assert compare_tensors(x, x.to(torch.int64)) == (True, 0.0, 0.0)
+    ok, a, _ = compare_tensors(x + torch.tensor([0, 1, 0], dtype=torch.int32), x.to(torch.int64))
+    assert not ok and a == 1.0
+    assert not compare_tensors(torch.zeros(3), torch.zeros(4))[0]
+    assert compare_tensors(torch.zeros(0, 5), torch.zeros(0, 5))[0]
+
+
+def _scan_case():
+    from cases.scan import make_case
+    return make_case(4, 300)
+
+
+def test_verify_all_passes_the_reference():
+    case = _scan_case()
+    ok, report = verify_all(case, case.reference_forward, device="cpu")
+    assert ok, report
+    assert "=== overall: PASS ===" in report and report.count("seed=") == 10
+
+
+def test_verify_all_catches_a_forward_mistake():
+    case = _scan_case()
+
+    def off_by_one_column(inputs, params):
+        y = case.reference_forward(inputs, params)
+        return torch.cat([y[:, :1] * 0, y[:, :-1]], dim=1)  # exclusive scan
+
+    ok, report = verify_all(case, off_by_one_column, device="cpu")
+    assert not ok and "[forward] FAIL" in report
+
+
+class _DoubledGrad(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x):
+        return x.cumsum(-1)
+
+    @staticmethod
+    def backward(ctx, g):
+        return 2 * g.flip(-1).cumsum(-1).flip(-1)
+
+
+def test_verify_all_catches_a_gradient_mistake():
+    case = _scan_case()
+    ok, report = verify_all(case, lambda inputs, params: _DoubledGrad.apply(inputs["X"]),
+                            device="cpu")
+    assert not ok
+    assert "[forward] PASS" in report and "[backward] FAIL" in report
