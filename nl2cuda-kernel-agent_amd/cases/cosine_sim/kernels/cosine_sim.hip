@@ -259,11 +259,10 @@ int cosine_sim_forward_f32(const float* A, const float* B, float* S, float* inv_
     if (st) return st;
     return launch_norms(B, inv_b, M, D, eps, stream);
   }
-  if (D == kD && nl2k::aligned16(A) && nl2k::aligned16(B)) {
+  nl2k::pairwise::FwdPlan fp;
+  if (D == kD && nl2k::aligned16(A) && nl2k::aligned16(B) &&
+      nl2k::pairwise::plan_forward(N, M, fp)) {
     const int vec_store = (M % 4 == 0) && nl2k::aligned16(S);
-    nl2k::pairwise::FwdPlan fp;
-    if (!nl2k::pairwise::plan_forward(N, M, fp))
-      return nl2k::fail(NL2K_ERR_OVERFLOW, "%s: too many tiles", who);
     hipLaunchKernelGGL(nl2k::pairwise::pair_fwd_d64_kernel<CosFwdOp>, dim3(fp.n_wg), dim3(256),
                        0, stream, A, B, S, (int)N, (int)M, CosFwdOp{eps}, fp.n_jt, fp.n_units,
                        fp.upw, vec_store, inv_a, inv_b);

@@ -201,11 +201,10 @@ int rbf_forward_f32(const float* X, const float* Y, float* K, int64_t N,
   if (!X || !Y || !K)
     return nl2k::fail(NL2K_ERR_NULL, "rbf_forward_f32: X, Y and K must be non-null");
 
-  if (D == kD && nl2k::aligned16(X) && nl2k::aligned16(Y)) {
+  nl2k::pairwise::FwdPlan fp;
+  if (D == kD && nl2k::aligned16(X) && nl2k::aligned16(Y) &&
+      nl2k::pairwise::plan_forward(N, M, fp)) {
     const int vec_store = (M % 4 == 0) && nl2k::aligned16(K);
-    nl2k::pairwise::FwdPlan fp;
-    if (!nl2k::pairwise::plan_forward(N, M, fp))
-      return nl2k::fail(NL2K_ERR_OVERFLOW, "rbf_forward_f32: too many tiles");
     hipLaunchKernelGGL(nl2k::pairwise::pair_fwd_d64_kernel<RbfFwdOp>, dim3(fp.n_wg), dim3(256),
                        0, stream, X, Y, K, (int)N, (int)M, RbfFwdOp{-gamma * kLog2e}, fp.n_jt,
                        fp.n_units, fp.upw, vec_store, nullptr, nullptr);

@@ -40,6 +40,9 @@ constexpr int kTileFloats = kTile * kLds;
 constexpr int kTargetRegions = 256;  // one backward workgroup per CU
 constexpr int kFwdWorkgroups = 512;  // two forward workgroups per CU
 constexpr int kFwdRows = 256;        // rows per forward unit (4 waves x 64)
+// The tile kernels index rows and columns with int, up to a tile or region
+// past the last one; larger N or M take the callers' generic (int64) kernels.
+constexpr int64_t kMaxTileDim = INT32_MAX - 1024;
 
 // ------------------------------------------------------------------ forward
 // Op interface:
@@ -213,6 +216,7 @@ struct FwdPlan {
 };
 
 inline bool plan_forward(int64_t N, int64_t M, FwdPlan& p) {
+  if (N > kMaxTileDim || M > kMaxTileDim) return false;
   p.n_jt = (int)ceil_div(M, kTile);
   const int64_t n_units64 = ceil_div(N, kFwdRows) * p.n_jt;
   if (n_units64 > INT32_MAX) return false;
@@ -884,7 +888,7 @@ struct BwdPlan {
 
 inline BwdPlan plan_backward(int64_t N, int64_t M, int64_t D, bool sums) {
   BwdPlan p;
-  if (D != kD || N <= 0 || M <= 0) return p;
+  if (D != kD || N <= 0 || M <= 0 || N > kMaxTileDim || M > kMaxTileDim) return p;
   p.fast = true;
   // Region edges above 256 would need more than 256 accumulator registers
   // per lane on the dY side (two waves per SIMD), so R stays <= 256.
