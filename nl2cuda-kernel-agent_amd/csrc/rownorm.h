@@ -26,9 +26,8 @@
 //  * Backward: a workgroup walks a contiguous block of rows, prefetching the
 //    next row's dy and x while it finishes the current one, and accumulates
 //    its partial dw (/ dbias) in registers.  The per-block partials ([G][D])
-//    are summed by rn_colsum_kernel in two stream-ordered passes (column
-//    slices x row groups, then the groups' rows), every sum in a fixed
-//    order, so dw and dbias are deterministic.
+//    are summed by rn_colsum_kernel in one stream-ordered pass, every sum
+//    in a fixed order, so dw and dbias are deterministic.
 //  * Any other shape uses generic kernels that re-read x: one workgroup per
 //    row for y / dx, and rn_bwd_generic_partial_kernel (64 columns x a group
 //    of rows per block) for the partial rows, then the same column sums.
@@ -44,8 +43,8 @@ namespace nl2k {
 namespace rownorm {
 
 constexpr int kBlock = 256;
-constexpr int kBwdBlocks = 512;       // level-1 partial rows of dw / dbias
-constexpr int kColsumMaxSplit = 32;   // row groups per column slice in rn_colsum_kernel
+constexpr int kBwdBlocks = 512;       // row-cached backward blocks = partial rows of dw / dbias
+constexpr int kColsumWaves = 16;      // waves of a column-sum workgroup (64 columns)
 constexpr int kGenericMaxSplit = 512; // partial rows of the generic path
 
 __device__ __forceinline__ float dot4(f32x4 a, f32x4 b) {
@@ -339,43 +338,52 @@ __global__ __launch_bounds__(kBlock) void rn_bwd_generic_partial_kernel(
   }
 }
 
-// Column sums of partial rows, deterministic: block (cs, g) covers 64
-// column units (T = float4: four columns per unit, T = float: one) of slice
-// cs and rows [g per, min(R, (g + 1) per)) of in_w (/ in_b) ([R][D]); wave w
-// takes rows a + w, a + w + 4, ... and the four waves combine in LDS, in a
-// fixed order, into row g of out_w (/ out_b).  Launched once with gridDim.y
-// = 1 (out = dw, dbias) or twice, the second pass summing the first's rows.
-// Stream order makes the first pass's rows visible to the second; a
-// last-block-finishes scheme would need a device-scope fence per block,
-// i.e. an L2 write-back per block on this multi-XCD part.
-template <typename T, bool TWO>
-__global__ __launch_bounds__(kBlock) void rn_colsum_kernel(
-    const float* __restrict__ in_w, const float* __restrict__ in_b, int64_t R,
-    int64_t D, int64_t per, float* __restrict__ out_w, float* __restrict__ out_b) {
-  constexpr int VC = sizeof(T) / sizeof(float);
-  __shared__ T sw[4][64], sb[4][64];
+// dw[c] (and dbias[c]) = sum over the R partial rows of column c.  A
+// workgroup of 16 waves owns 64 columns: wave w sums rows w, w + 16, ... of
+// its lane's column, eight loads in flight per batch, and the 16 wave sums
+// combine in LDS in a fixed order.  One pass: a second launch of a small
+// kernel costs about 4 us of launch and drain on this part, more than the
+// partial rows take to read.  Stream order makes the partial rows visible.
+template <bool TWO>
+__global__ __launch_bounds__(64 * kColsumWaves) void rn_colsum_kernel(
+    const float* __restrict__ in_w, const float* __restrict__ in_b, int64_t R, int64_t D,
+    float* __restrict__ out_w, float* __restrict__ out_b) {
+  __shared__ float sw[kColsumWaves][64], sb[kColsumWaves][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t DU = D / VC;
-  const int64_t cu = (int64_t)blockIdx.x * 64 + lane;
-  const int64_t cc = min(cu, DU - 1);
-  const T* iw = reinterpret_cast<const T*>(in_w);
-  const T* ib = reinterpret_cast<const T*>(in_b);
-  const int64_t a = (int64_t)blockIdx.y * per, e = min(R, a + per);
-  T aw = (T)0.f, ab = (T)0.f;
-#pragma unroll 4
-  for (int64_t r = a + wave; r < e; r += 4) {
-    aw += iw[r * DU + cc];
-    if constexpr (TWO) ab += ib[r * DU + cc];
+  const int64_t c = (int64_t)blockIdx.x * 64 + lane;
+  const int64_t cc = min(c, D - 1);
+  float aw = 0.f, ab = 0.f;
+  int64_t r = wave;
+  for (; r + 7 * kColsumWaves < R; r += 8 * kColsumWaves) {
+    float vw[8], vb[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      vw[k] = in_w[(r + k * kColsumWaves) * D + cc];
+      if constexpr (TWO) vb[k] = in_b[(r + k * kColsumWaves) * D + cc];
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the batch's loads issue before the adds
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      aw += vw[k];
+      if constexpr (TWO) ab += vb[k];
+    }
+  }
+  for (; r < R; r += kColsumWaves) {
+    aw += in_w[r * D + cc];
+    if constexpr (TWO) ab += in_b[r * D + cc];
   }
   sw[wave][lane] = aw;
   if constexpr (TWO) sb[wave][lane] = ab;
   __syncthreads();
-  if (wave == 0 && cu < DU) {
-    reinterpret_cast<T*>(out_w)[blockIdx.y * DU + cu] =
-        (sw[0][lane] + sw[1][lane]) + (sw[2][lane] + sw[3][lane]);
-    if constexpr (TWO)
-      reinterpret_cast<T*>(out_b)[blockIdx.y * DU + cu] =
-          (sb[0][lane] + sb[1][lane]) + (sb[2][lane] + sb[3][lane]);
+  if (wave == 0 && c < D) {
+    float tw = 0.f, tb = 0.f;
+#pragma unroll
+    for (int w = 0; w < kColsumWaves; ++w) {
+      tw += sw[w][lane];
+      if constexpr (TWO) tb += sb[w][lane];
+    }
+    out_w[c] = tw;
+    if constexpr (TWO) out_b[c] = tb;
   }
 }
 
@@ -396,8 +404,6 @@ struct Plan {
   int v = 4;            // float4 per thread
   int64_t G = 0;        // partial rows of dw / dbias
   int64_t rpb = 0;      // rows per block: backward blocks (cached) or partial groups (generic)
-  int64_t S = 0;        // row groups per column slice in rn_colsum_kernel
-  int64_t cper = 0;     // partial rows per such group
 };
 
 inline Plan plan(int64_t B, int64_t D, bool aligned) {
@@ -425,22 +431,14 @@ inline Plan plan(int64_t B, int64_t D, bool aligned) {
     p.rpb = std::max<int64_t>(1, ceil_div(B, s1));
   }
   p.G = B > 0 ? ceil_div(B, p.rpb) : 0;
-  // column sums: ~512 blocks of 256 columns (float4) x (G / S) partial rows
-  const int64_t slices4 = ceil_div(D, 256);
-  const int64_t s2 = std::min<int64_t>(
-      std::min<int64_t>(std::max<int64_t>(1, ceil_div(512, slices4)), kColsumMaxSplit),
-      std::max<int64_t>(p.G, 1));
-  p.cper = std::max<int64_t>(1, ceil_div(p.G, s2));
-  p.S = p.G > 0 ? ceil_div(p.G, p.cper) : 0;
   return p;
 }
 
-// Workspace: partial rows (n G D, n = 2 with a bias, else 1) and, when the
-// column sums take two passes, the first pass's rows (n S D).
+// Workspace: the partial rows, n G D floats (n = 2 with a bias, else 1).
 template <class P>
 size_t workspace_floats(int64_t D, const Plan& p) {
   const int64_t n = P::kBias ? 2 : 1;
-  return (size_t)(n * p.G * D + (p.S > 1 ? n * p.S * D : 0));
+  return (size_t)(n * p.G * D);
 }
 
 template <class P>
@@ -503,8 +501,6 @@ int run_backward(const float* dy, const float* x, const float* w, const float* s
   const Plan p = plan(B, D, aligned);
   float* pw = ws;
   float* pb = pw + p.G * D;
-  float* l2w = P::kBias ? pb + p.G * D : pb;
-  float* l2b = l2w + p.S * D;
   int st;
   if (p.cached) {
 #define RN_BWD(V)                                                                            \
@@ -534,25 +530,8 @@ int run_backward(const float* dy, const float* x, const float* w, const float* s
     st = check_launch(who);
   }
   if (st) return st;
-  const bool vec = D % 4 == 0 && aligned16(dw) && (!P::kBias || aligned16(dbias));
-  const unsigned slices = (unsigned)ceil_div(D, vec ? 256 : 64);
-  auto colsum = [&](const float* iw, const float* ib, int64_t R, int64_t per, unsigned groups,
-                    float* ow, float* ob) {
-    if (vec)
-      hipLaunchKernelGGL((rn_colsum_kernel<f32x4, P::kBias>), dim3(slices, groups), dim3(kBlock),
-                         0, stream, iw, ib, R, D, per, ow, ob);
-    else
-      hipLaunchKernelGGL((rn_colsum_kernel<float, P::kBias>), dim3(slices, groups), dim3(kBlock),
-                         0, stream, iw, ib, R, D, per, ow, ob);
-  };
-  if (p.S > 1) {
-    colsum(pw, pb, p.G, p.cper, (unsigned)p.S, l2w, l2b);
-    st = check_launch(who);
-    if (st) return st;
-    colsum(l2w, l2b, p.S, p.S, 1u, dw, dbias);
-  } else {
-    colsum(pw, pb, p.G, p.G, 1u, dw, dbias);
-  }
+  hipLaunchKernelGGL((rn_colsum_kernel<P::kBias>), dim3((unsigned)ceil_div(D, 64)),
+                     dim3(64 * kColsumWaves), 0, stream, pw, pb, p.G, D, dw, dbias);
   return check_launch(who);
 }
 
