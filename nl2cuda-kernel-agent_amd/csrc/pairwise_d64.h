@@ -568,14 +568,16 @@ __global__ __launch_bounds__(512) void pair_bwd_d64_kernel(
 // role its own live ranges (168 VGPRs, three waves per SIMD).
 template <class Op, int JC, bool kVecNM>
 __global__ __launch_bounds__(768) void pair_bwd_d64_3r_kernel(
-    const float* __restrict__ X, const float* __restrict__ Y,
+    const float* X, const float* __restrict__ Y,
     const float* dK, const float* Kf,
     float* __restrict__ Px, float* __restrict__ Rx, float* __restrict__ Py,
     float* __restrict__ Ry, int N, int M, int RI, int nRJ,
-    const float* __restrict__ sx, const float* __restrict__ sy) {
-  // dK and Kf are deliberately not __restrict__: with it the compiler treats
-  // their loads as invariant and sinks the prefetch of tile t+2 past the
-  // workgroup barriers to its use, which serialises the memory latency.
+    const float* sx, const float* __restrict__ sy) {
+  // X, sx, dK and Kf are deliberately not __restrict__: with it the compiler
+  // treats their loads as invariant and sinks a prefetch past the workgroup
+  // barriers to its use (for dK / K, tile t+2's, which serialises the memory
+  // latency; for X, the reload before the staging loop, which leaves the
+  // loop's wait counts pessimistic).
   constexpr int RJ = JC * kTile;
   constexpr int kYtLds = RJ + 4;
   __shared__ __attribute__((aligned(16))) float P[2][kTileFloats];
@@ -597,6 +599,16 @@ __global__ __launch_bounds__(768) void pair_bwd_d64_3r_kernel(
   const int n_ic = (rows + kTile - 1) / kTile;
   const int n_jc = (cols + kTile - 1) / kTile;
   const int n_tiles = n_ic * n_jc;
+  // Skewed walk: region (ri, rj) visits its i-chunks starting at rj mod n_ic
+  // and its j-chunks starting at ri mod n_jc.  With every region on the same
+  // walk, the concurrent dK / K reads of all CUs share their address bits
+  // and crowd the same memory channels; a 4096^2 read in 64 x 64 tiles took
+  // 16.1 us in lockstep and 13.1 us skewed (12.2 us as whole rows).  The
+  // walk position, not the chunk, selects the double buffers; the column
+  // accumulators are kept per walk position and mapped back at the flush.
+  const int ic0 = rj % n_ic, jc0 = ri % n_jc;
+  auto chunk_at = [&](int pos) { return pos + ic0 < n_ic ? pos + ic0 : pos + ic0 - n_ic; };
+  auto col_at = [&](int pos) { return pos + jc0 < n_jc ? pos + jc0 : pos + jc0 - n_jc; };
 
   // Staging-wave state (declared for all waves; only waves 8-11 use it).
   const int ptid = tid - 512;
@@ -610,7 +622,8 @@ __global__ __launch_bounds__(768) void pair_bwd_d64_3r_kernel(
   float g_xs;
   bool g_ok[3][4];
   auto load_stage = [&](int t, f32x4 (&dk)[4], f32x4 (&kk)[4], bool (&ok)[4]) {
-    const int ic = t / n_jc, jc = t - ic * n_jc;
+    const int pi = t / n_jc;
+    const int ic = chunk_at(pi), jc = col_at(t - pi * n_jc);
     const int ib = ibase + ic * kTile;
     const int jb = jbase + jc * kTile;
 #pragma unroll
@@ -650,14 +663,14 @@ __global__ __launch_bounds__(768) void pair_bwd_d64_3r_kernel(
         store4(&dst[(srow + 16 * s) * kLds + scol], ok[s] ? dk[s] : zero4());
     }
   };
-  auto load_x = [&](int ic, f32x4 (&xs)[4], float& sc) {
-    const size_t r = (size_t)min(ibase + ic * kTile + xrow, N - 1);
+  auto load_x = [&](int pos, f32x4 (&xs)[4], float& sc) {
+    const size_t r = (size_t)min(ibase + chunk_at(pos) * kTile + xrow, N - 1);
 #pragma unroll
     for (int s = 0; s < 4; ++s) xs[s] = load4(X + r * kD + xcol + 16 * s);
     if constexpr (Op::kScale) sc = sx[r];
   };
-  auto commit_x = [&](int ic, const f32x4 (&xs)[4], float sc) {
-    float* dst = Xt[ic & 1];
+  auto commit_x = [&](int pos, const f32x4 (&xs)[4], float sc) {
+    float* dst = Xt[pos & 1];
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -668,8 +681,9 @@ __global__ __launch_bounds__(768) void pair_bwd_d64_3r_kernel(
           dst[(xcol + 16 * s + u) * kLds + xrow] = xs[s][u];
       }
   };
-  // X chunk published at step t: the one after the chunk of tile t (clamped;
-  // at the last chunk that rewrites the chunk in use with identical bits).
+  // X chunk (walk position) published at step t: the one after tile t's
+  // (clamped; at the last chunk that rewrites the chunk in use with
+  // identical bits).
   auto x_chunk = [&](int t) { return min(t / n_jc + 1, n_ic - 1); };
 
   // Tile 0's loads go out first, then waves 0-7 stage the region's Y rows
@@ -724,10 +738,18 @@ __global__ __launch_bounds__(768) void pair_bwd_d64_3r_kernel(
     // statically (the loop is unrolled by three): a runtime stage index would
     // be if-converted into selects on the loaded data, forcing a wait right
     // after each load.
+    // The X reload goes out before tiles 1 and 2 (the barrier keeps the
+    // compiler from hoisting their loads above it): the loop then starts
+    // with the same order of outstanding loads as every later pass, and the
+    // wait counts at the loop head stay as tight as in the body.  Otherwise
+    // the loop's first step of every three waited for the previous step's
+    // tiles.
     commit_x(0, g_x, g_xs);
     load_x(x_chunk(0), g_x, g_xs);
+    __builtin_amdgcn_sched_barrier(0);
     load_stage(min(1, n_tiles - 1), g_dk[1], g_k[1], g_ok[1]);
     load_stage(min(2, n_tiles - 1), g_dk[2], g_k[2], g_ok[2]);
+    __builtin_amdgcn_sched_barrier(0);
     commit_stage(0, g_dk[0], g_k[0], g_ok[0]);
     __syncthreads();
     auto step = [&](int t, f32x4 (&ldk)[4], f32x4 (&lk)[4], bool (&lok)[4],
@@ -754,17 +776,18 @@ __global__ __launch_bounds__(768) void pair_bwd_d64_3r_kernel(
   if (wave < 4) {
     // (W.Y)^T rows 16 wb.. of every tile, accumulated over the region's
     // columns and flushed per i-chunk (dX side).
-    for (int ic = 0; ic < n_ic; ++ic) {
+    for (int pi = 0; pi < n_ic; ++pi) {
+      const int ic = chunk_at(pi);
       f32x4 accX[4];
 #pragma unroll
       for (int db = 0; db < 4; ++db) accX[db] = zero4();
       float rp = 0.f;
 #pragma unroll
-      for (int jc = 0; jc < JC; ++jc) {
-        if (jc < n_jc) {
-          const int t = ic * n_jc + jc;
+      for (int pj = 0; pj < JC; ++pj) {
+        if (pj < n_jc) {
+          const int t = pi * n_jc + pj;
           const float* Pb = P[t & 1];
-          const float* Yb = Yt + jc * kTile;
+          const float* Yb = Yt + col_at(pj) * kTile;
           f32x4 xa[2], xbv[2][4];
           xa[0] = load4(&Pb[(wb * 16 + n) * kLds + 4 * h]);
 #pragma unroll
@@ -818,12 +841,12 @@ __global__ __launch_bounds__(768) void pair_bwd_d64_3r_kernel(
 #pragma unroll
     for (int db = 0; db < 4; ++db) accY[c][db] = zero4();
   }
-  for (int ic = 0; ic < n_ic; ++ic) {
-    const float* Xb = Xt[ic & 1];
+  for (int pi = 0; pi < n_ic; ++pi) {
+    const float* Xb = Xt[pi & 1];
 #pragma unroll
-    for (int jc = 0; jc < JC; ++jc) {
+    for (int jc = 0; jc < JC; ++jc) {  // walk position; column chunk col_at(jc)
       if (jc < n_jc) {
-        const int t = ic * n_jc + jc;
+        const int t = pi * n_jc + jc;
         const float* Pb = P[t & 1];
         f32x4 yb[2][4];
         float ya[2][4];
@@ -858,7 +881,7 @@ __global__ __launch_bounds__(768) void pair_bwd_d64_3r_kernel(
 #pragma unroll
   for (int jc = 0; jc < JC; ++jc) {
     if (jc < n_jc) {
-      const int j_base = jbase + jc * kTile + wb * 16;
+      const int j_base = jbase + col_at(jc) * kTile + wb * 16;
       if constexpr (Op::kSums) {
         float cs = cp[jc];
         cs += __shfl_xor(cs, 16, 64);
