@@ -205,9 +205,9 @@ def main():
 
     fwd_tf = ff / (fwd_avg * 1e-3) / 1e12
     bwd_tf = bf / (bwd_avg * 1e-3) / 1e12
-    traffic = None
+    traffic = None  # measured for the 4096 workload only
     tpath = os.path.join(REPO, "profiles", "rbf_bwd_4096_traffic.json")
-    if os.path.exists(tpath):
+    if n == 4096 and m == 4096 and d == 64 and os.path.exists(tpath):
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
 
