@@ -56,7 +56,12 @@ constexpr int kThreads = 256;
 constexpr int kPer = 4;                 // positions per lane per step
 constexpr int kStep = 64 * kPer;        // positions per wave step
 constexpr int kWin = 512;               // row starts staged per LDS window (per wave)
-constexpr int64_t kWaveItems = 4096;    // rows + nonzeros per wave (D == 1)
+// Rows + nonzeros per wave (D == 1).  Halving the forward's range (more
+// waves, more gathers in flight per CU) took the forward from 150 to 142 us
+// and the dvals + dX backward from 269 to 260 us; the dX-only backward is
+// best with the longer range (143 against 147 us).
+constexpr int64_t kWaveItemsShort = 2048;
+constexpr int64_t kWaveItemsLong = 4096;
 
 template <typename I>
 __device__ __forceinline__ int64_t ld_ptr(const I* __restrict__ ptr, int64_t r, int64_t nnz) {
@@ -177,8 +182,9 @@ struct Walk {
 template <typename I>
 __device__ __forceinline__ bool walk_begin(const I* __restrict__ ptr, int64_t M, int64_t nnz,
                                            int64_t w, int64_t n_waves, int lane, Walk& s) {
-  s.r0 = w == 0 ? 0 : rows_lower_bound(ptr, M, nnz, w * kWaveItems, lane);
-  s.r1 = w == n_waves - 1 ? M : rows_lower_bound(ptr, M, nnz, (w + 1) * kWaveItems, lane);
+  const int64_t per = (nnz + M + n_waves - 1) / n_waves;  // items per wave
+  s.r0 = w == 0 ? 0 : rows_lower_bound(ptr, M, nnz, w * per, lane);
+  s.r1 = w == n_waves - 1 ? M : rows_lower_bound(ptr, M, nnz, (w + 1) * per, lane);
   if (s.r1 <= s.r0) return false;
   s.pos = ld_ptr(ptr, s.r0, nnz);
   s.b = max(s.pos, ld_ptr(ptr, s.r1, nnz));
@@ -801,7 +807,7 @@ int forward(const I* ptr, const I* col, const float* vals, const float* X, float
   if (!ptr || !X || !Y || (nnz > 0 && (!col || !vals)))
     return nl2k::fail(NL2K_ERR_NULL, "%s: null pointer argument", who);
   if (D == 1) {
-    const int64_t n_waves = std::max<int64_t>(1, nl2k::ceil_div(nnz + M, kWaveItems));
+    const int64_t n_waves = std::max<int64_t>(1, nl2k::ceil_div(nnz + M, kWaveItemsShort));
     const int64_t blocks = nl2k::ceil_div(n_waves, kThreads / 64);
     if (blocks > INT32_MAX) return nl2k::fail(NL2K_ERR_OVERFLOW, "%s: too many rows", who);
     const bool vec = nl2k::aligned16(col) && nl2k::aligned16(vals);
@@ -901,8 +907,9 @@ int backward(const I* ptr, const I* col, const float* vals, const float* X, cons
     if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
       return nl2k::fail(NL2K_ERR_ALIGN, "%s: workspace must be 256-byte aligned", who);
   }
+  const int64_t wave_items = dvals ? kWaveItemsShort : kWaveItemsLong;
   if (sorted_dx) {
-    const int64_t n_waves = std::max<int64_t>(1, nl2k::ceil_div(nnz + M, kWaveItems));
+    const int64_t n_waves = std::max<int64_t>(1, nl2k::ceil_div(nnz + M, wave_items));
     const int64_t blocks = nl2k::ceil_div(n_waves, kThreads / 64);
     if (blocks > INT32_MAX || bp.n_tiles > INT32_MAX)
       return nl2k::fail(NL2K_ERR_OVERFLOW, "%s: too many rows", who);
@@ -939,7 +946,7 @@ int backward(const I* ptr, const I* col, const float* vals, const float* X, cons
   }
   if (M == 0 || nnz == 0 || (!dX && !dvals)) return nl2k::succeed();
   if (D == 1) {
-    const int64_t n_waves = std::max<int64_t>(1, nl2k::ceil_div(nnz + M, kWaveItems));
+    const int64_t n_waves = std::max<int64_t>(1, nl2k::ceil_div(nnz + M, wave_items));
     const int64_t blocks = nl2k::ceil_div(n_waves, kThreads / 64);
     if (blocks > INT32_MAX) return nl2k::fail(NL2K_ERR_OVERFLOW, "%s: too many rows", who);
     const bool vec = nl2k::aligned16(col) && nl2k::aligned16(vals) &&
