@@ -120,7 +120,8 @@ def main():
 
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the RBF path is single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "(the RBF path is single-GPU; sharded, each GPU would take a block of X rows against "
+              "all of Y and one all-reduce would sum dY)", file=sys.stderr)
         return 2
 
     import torch
