@@ -10,8 +10,9 @@
  * allocates nothing, keeps no state, never synchronises and launches on
  * `stream`.  Arguments are validated before any HIP call (NL2K_* codes,
  * message from softmax_ce_last_error()).  The loss is deterministic: one
- * partial sum per workgroup (in the caller's scratch workspace), added in a
- * fixed order by a second, one-workgroup kernel (no float atomics).  A
+ * partial sum per workgroup, published in the caller's scratch workspace
+ * and added in a fixed order by workgroup 0 of the same launch (no float
+ * atomics, one launch).  A
  * label outside [0, C) is not checked on the host (labels live on the
  * device); it makes the loss and that row's gradient NaN.  B == 0 gives
  * loss = NaN (the mean of no terms).
@@ -37,9 +38,10 @@
 extern "C" {
 #endif
 
-/* Scratch bytes softmax_ce_forward_f32 needs (4-byte aligned; a constant
- * 4096: one float for each of at most 1024 workgroups); 0 for invalid
- * sizes. */
+/* Scratch bytes softmax_ce_forward_f32 needs (8-byte aligned; a constant
+ * 16384: a 16-byte slot pair for each of at most 1024 workgroups, tagged
+ * with a fresh nonce per call, so no initial contents are needed); 0 for
+ * invalid sizes. */
 size_t softmax_ce_forward_workspace_bytes(int64_t B, int64_t C);
 
 /* loss [1] and lse [B] (softmax_ce_forward.cu:52-65, `softmax_ce_forward`;

@@ -29,21 +29,15 @@
 //    its chunks in increasing order and publishes before it waits, so the
 //    lowest unpublished chunk can always make progress.
 //  * Slots need no clearing, so a call is a single launch and the workspace
-//    needs no initial contents: every call draws a fresh 64-bit nonce n on
-//    the host (a process-wide counter, never 0) and two masks m0 and
-//    m1 = m0 ^ n; a slot is two words, v ^ m0 and v ^ m1, each written with
-//    one relaxed agent-scope atomic store.  A reader accepts the pair only
-//    when the two words XOR to n: a slot left complete by an earlier call
-//    XORs to that call's nonce and a zeroed one to 0, so neither passes; a
-//    pair read half-written, or never-written memory, passes only by chance
-//    (probability 2^-64 per read, as the masks are hashes of n).
+//    needs no initial contents: the slots are tagged with a fresh 64-bit
+//    nonce per call (csrc/nonce_slots.h), and a reader takes only pairs this
+//    call wrote.
 //  * Reverse scans mirror the positions: logical p <-> physical D - 1 - p.
 #include <algorithm>
-#include <atomic>
-#include <chrono>
 #include <cstdint>
 
 #include "../../../csrc/common.h"
+#include "../../../csrc/nonce_slots.h"
 #include "scan.h"
 
 using nl2k::f32x4;
@@ -62,10 +56,7 @@ constexpr int kResidentBlocks = 1024;           // 256 CUs x 4 workgroups
 constexpr unsigned kSpinLimit = 1u << 24;       // hang guard for the carry wait
 
 // ------------------------------------------------ 64-bit accumulator helpers
-// The call's slot masks (m1 = m0 ^ nonce).
-struct SlotKey {
-  unsigned long long m0, m1;
-};
+using SlotKey = nl2k::slots::Key;
 
 template <typename T>
 __device__ __forceinline__ unsigned long long bits64(T v) {
@@ -233,41 +224,36 @@ __device__ __forceinline__ void emit_tile(const TileScan<In, Acc>& s, Acc base, 
   }
 }
 
-// Publishes a chunk total in slot pair p (two words, see the header).
+// Publishes a chunk total in slot pair p (csrc/nonce_slots.h).
 template <typename Acc>
 __device__ __forceinline__ void publish(unsigned long long* __restrict__ slots, int p, Acc v,
                                         SlotKey key) {
-  const unsigned long long b = bits64(v);
-  __hip_atomic_store(slots + 2 * p, b ^ key.m0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_store(slots + 2 * p + 1, b ^ key.m1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  nl2k::slots::publish(slots, p, bits64(v), key);
 }
 
 // Sum of the totals of chunks [0, chunk) of a row, in a fixed order (wave 0).
 template <typename Acc>
 __device__ Acc carry_in(const unsigned long long* __restrict__ slots, int chunk, int lane,
                         SlotKey key, unsigned* __restrict__ err) {
-  const unsigned long long tag = key.m0 ^ key.m1;  // the call's nonce
   Acc carry = (Acc)0;
   for (int base = 0; base < chunk; base += 64) {
     const int p = base + lane;
     Acc v = (Acc)0;
     if (p < chunk) {
-      unsigned long long w0 =
-          __hip_atomic_load(slots + 2 * p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      unsigned long long w1 =
-          __hip_atomic_load(slots + 2 * p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      unsigned long long w0 = nl2k::slots::load_word(slots + 2 * p);
+      unsigned long long w1 = nl2k::slots::load_word(slots + 2 * p + 1);
       unsigned spins = 0;
-      while ((w0 ^ w1) != tag) {
+      while (!nl2k::slots::ready(w0, w1, key)) {
         if (++spins > kSpinLimit) {  // never expected: report and give up
           __hip_atomic_fetch_add(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           w0 = key.m0;  // reads as 0
           break;
         }
         __builtin_amdgcn_s_sleep(1);
-        w0 = __hip_atomic_load(slots + 2 * p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        w1 = __hip_atomic_load(slots + 2 * p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        w0 = nl2k::slots::load_word(slots + 2 * p);
+        w1 = nl2k::slots::load_word(slots + 2 * p + 1);
       }
-      v = from_bits64<Acc>(w0 ^ key.m0);
+      v = from_bits64<Acc>(nl2k::slots::decode(w0, key));
     }
     carry += wave_total(v);
   }
@@ -378,23 +364,6 @@ size_t workspace_bytes(const Plan& p) {
   return p.slots > 0 ? (size_t)p.slots * 16 + 8 : 0;
 }
 
-// A fresh nonce per call (process-wide, never 0; seeded from the clock so a
-// reloaded library does not repeat an earlier run's nonces) and its masks.
-unsigned long long splitmix64(unsigned long long z) {
-  z += 0x9E3779B97F4A7C15ull;
-  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-  return z ^ (z >> 31);
-}
-
-SlotKey next_key() {
-  static std::atomic<unsigned long long> counter{
-      splitmix64((unsigned long long)std::chrono::steady_clock::now().time_since_epoch().count())};
-  unsigned long long n = counter.fetch_add(1, std::memory_order_relaxed);
-  if (n == 0) n = counter.fetch_add(1, std::memory_order_relaxed);
-  const unsigned long long m0 = splitmix64(n ^ 0xD1B54A32D192ED03ull);
-  return SlotKey{m0, m0 ^ n};
-}
 
 int validate(int64_t rows, int64_t D, const char* who) {
   if (rows < 0 || D < 1)
@@ -426,7 +395,7 @@ int run(const In* x, Out* y, int64_t rows, int64_t D, void* workspace, size_t ws
       return nl2k::fail(NL2K_ERR_ALIGN, "%s: workspace must be 8-byte aligned", who);
     slots = static_cast<unsigned long long*>(workspace);
     err = reinterpret_cast<unsigned*>(slots + 2 * p.slots);
-    key = next_key();
+    key = nl2k::slots::next_key();
   }
   const bool vec = D % 4 == 0 && nl2k::aligned16(x) && nl2k::aligned16(y);
   // Single-chunk rows never wait, so their grid is not capped.

@@ -16,11 +16,13 @@
 //    issues the loads of R rows before using any.  The row max, then sum
 //    exp2((x - max) log2 e), reduced with DPP lane moves (plus one LDS step
 //    for TPR = 256); the label's logit is loaded directly.  At most 1024
-//    workgroups stride over the rows; each writes lse per row and one partial
-//    loss sum, and a one-workgroup finalize kernel adds the partials in a
-//    fixed order, so the loss is deterministic (a last-workgroup reduction
-//    through agent-scope slots in the same launch measured slower: its
-//    serial slot round trips outlast the second launch).
+//    workgroups stride over the rows; each writes lse per row and publishes
+//    one partial loss sum in a nonce-tagged slot pair (csrc/nonce_slots.h),
+//    and workgroup 0 waits for all of them and adds them in a fixed order,
+//    so the loss is deterministic and the forward is one launch.  Only
+//    workgroup 0 waits, on workgroups that never wait.  (A last-arriving-
+//    workgroup scheme with a shared counter measured slower: 1024 atomics on
+//    one address serialise.)
 //  * Backward: lse saved by the forward turns the gradient into a pure
 //    streaming pass (read logits, write dlogits, no reductions), laid out
 //    like the forward so each row's lse and label are read once.
@@ -34,6 +36,7 @@
 #include <cstdint>
 
 #include "../../../csrc/common.h"
+#include "../../../csrc/nonce_slots.h"
 #include "softmax_ce.h"
 
 using nl2k::f32x4;
@@ -44,9 +47,12 @@ constexpr int kBlock = 256;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kFwdBlocks = 1024;  // most forward workgroups (one partial loss each)
-static_assert(kFwdBlocks % 256 == 0, "the finalize kernel reads kFwdBlocks / 256 per thread");
-// Workspace of the forward: one partial loss per workgroup.
-constexpr size_t kWorkspaceBytes = sizeof(float) * (size_t)kFwdBlocks;
+static_assert(kFwdBlocks % 256 == 0, "the loss sum reads kFwdBlocks / 256 slots per thread");
+// Workspace of the forward: one nonce-tagged slot pair (16 bytes) per
+// workgroup's partial loss.
+constexpr size_t kWorkspaceBytes = 16 * (size_t)kFwdBlocks;
+constexpr unsigned kSpinLimit = 1u << 24;  // hang guard for workgroup 0's wait
+
 
 // Reduce N values per thread over the TPR threads that share a row (TPR = 64:
 // one wave; TPR = 256: the workgroup, through `red`, >= 4 * N floats); the
@@ -83,17 +89,56 @@ constexpr int rows_in_flight() {
   return V == 1 ? 8 : V == 2 ? 4 : 2;
 }
 
+// Workgroup 0, after its own rows: waits for the n partial losses of this
+// call (slot pairs 0 .. n-1) and writes loss = (their sum, in a fixed order)
+// / B.  Only this workgroup waits, and only for workgroups that never wait,
+// so the wait ends whatever the residency; the spin cap (never expected)
+// gives a NaN loss instead of a hang.  Thread t adds slots t + 256 j in j
+// order, then the workgroup reduction: the same additions a separate
+// one-workgroup kernel over the partials would make.
+__device__ void sum_partials(const unsigned long long* __restrict__ slots, nl2k::slots::Key key,
+                             int n, int64_t B, float* __restrict__ loss, float* red) {
+  constexpr int kPer = kFwdBlocks / kBlock;
+  float x[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int p = (int)threadIdx.x + j * kBlock;
+    x[j] = 0.f;
+    if (p < n) {
+      unsigned long long w0 = nl2k::slots::load_word(slots + 2 * p);
+      unsigned long long w1 = nl2k::slots::load_word(slots + 2 * p + 1);
+      unsigned spins = 0;
+      while (!nl2k::slots::ready(w0, w1, key)) {
+        if (++spins > kSpinLimit) {
+          w0 = key.m0 ^ (unsigned long long)__float_as_uint(NAN);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        w0 = nl2k::slots::load_word(slots + 2 * p);
+        w1 = nl2k::slots::load_word(slots + 2 * p + 1);
+      }
+      x[j] = __uint_as_float((unsigned)nl2k::slots::decode(w0, key));
+    }
+  }
+  float s[1] = {0.f};
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) s[0] += (int)threadIdx.x + j * kBlock < n ? x[j] : 0.f;
+  row_reduce<kBlock, 1, false>(s, red);
+  if (threadIdx.x == 0) loss[0] = s[0] / (float)B;
+}
+
 // Row-cached forward.  TPR threads own a row and keep its V float4 per
 // thread in registers; a block step covers R row groups of kBlock / TPR rows
 // (all R rows' loads issued before any is used), block steps are strided by
 // the grid.  Rows past B are clamped to B - 1 for the loads and discarded.
 // Thread 0 of each row group keeps its rows' loss terms in row order; the
-// workgroup's sum (groups added in a fixed order) goes to
-// partial[blockIdx.x].
+// workgroup's sum (groups added in a fixed order) is published in slot pair
+// blockIdx.x, and workgroup 0 then adds all partials (sum_partials).
 template <int TPR, int V, bool FULL>
 __global__ __launch_bounds__(kBlock) void sce_fwd_kernel(
     const float* __restrict__ logits, const int64_t* __restrict__ labels,
-    float* __restrict__ lse_out, float* __restrict__ partial, int64_t B, int C) {
+    float* __restrict__ lse_out, unsigned long long* __restrict__ slots, nl2k::slots::Key key,
+    float* __restrict__ loss, int64_t B, int C) {
   constexpr int R = rows_in_flight<V>();
   constexpr int RPB = kBlock / TPR;
   constexpr int RPI = RPB * R;
@@ -171,15 +216,17 @@ __global__ __launch_bounds__(kBlock) void sce_fwd_kernel(
     float wg = 0.f;
 #pragma unroll
     for (int g = 0; g < RPB; ++g) wg += sacc[g];
-    partial[blockIdx.x] = wg;
+    nl2k::slots::publish(slots, blockIdx.x, __float_as_uint(wg), key);
   }
+  if (blockIdx.x == 0) sum_partials(slots, key, (int)gridDim.x, B, loss, red);
 }
 
 // Generic forward (any C and alignment): workgroups stride over the rows,
 // one row at a time, two passes over it (max, then the sum of exp).
 __global__ __launch_bounds__(kBlock) void sce_fwd_generic_kernel(
     const float* __restrict__ logits, const int64_t* __restrict__ labels,
-    float* __restrict__ lse_out, float* __restrict__ partial, int64_t B, int64_t C) {
+    float* __restrict__ lse_out, unsigned long long* __restrict__ slots, nl2k::slots::Key key,
+    float* __restrict__ loss, int64_t B, int64_t C) {
   __shared__ float red[4];
   float acc = 0.f;
   for (int64_t row = blockIdx.x; row < B; row += gridDim.x) {
@@ -198,25 +245,8 @@ __global__ __launch_bounds__(kBlock) void sce_fwd_generic_kernel(
       acc += lab >= 0 ? lse - xr[lab] : NAN;
     }
   }
-  if (threadIdx.x == 0) partial[blockIdx.x] = acc;
-}
-
-// loss = (sum of the n <= kFwdBlocks partials, added in a fixed order) / B.
-// Every thread issues its kFwdBlocks / kBlock loads (clamped addresses)
-// before adding any, so the kernel waits for one memory round trip.
-__global__ __launch_bounds__(kBlock) void sce_finalize_kernel(const float* __restrict__ partial,
-                                                              int n, int64_t B,
-                                                              float* __restrict__ loss) {
-  constexpr int kPer = kFwdBlocks / kBlock;
-  __shared__ float red[4];
-  float x[kPer];
-#pragma unroll
-  for (int j = 0; j < kPer; ++j) x[j] = partial[min((int)threadIdx.x + j * kBlock, n - 1)];
-  float s[1] = {0.f};
-#pragma unroll
-  for (int j = 0; j < kPer; ++j) s[0] += (int)threadIdx.x + j * kBlock < n ? x[j] : 0.f;
-  row_reduce<kBlock, 1, false>(s, red);
-  if (threadIdx.x == 0) loss[0] = s[0] / (float)B;
+  if (threadIdx.x == 0) nl2k::slots::publish(slots, blockIdx.x, __float_as_uint(acc), key);
+  if (blockIdx.x == 0) sum_partials(slots, key, (int)gridDim.x, B, loss, red);
 }
 
 // Row-cached backward, laid out like the forward: TPR threads per row, V
@@ -377,9 +407,10 @@ int softmax_ce_forward_f32(const float* logits, const int64_t* labels, float* lo
   if (!workspace || workspace_bytes < kWorkspaceBytes)
     return nl2k::fail(NL2K_ERR_WORKSPACE, "%s: workspace of %zu bytes required, got %zu", who,
                       kWorkspaceBytes, workspace ? workspace_bytes : (size_t)0);
-  if (reinterpret_cast<uintptr_t>(workspace) % 4 != 0)
-    return nl2k::fail(NL2K_ERR_ALIGN, "%s: workspace must be 4-byte aligned", who);
-  float* partial = static_cast<float*>(workspace);
+  if (reinterpret_cast<uintptr_t>(workspace) % 8 != 0)
+    return nl2k::fail(NL2K_ERR_ALIGN, "%s: workspace must be 8-byte aligned", who);
+  unsigned long long* slots = static_cast<unsigned long long*>(workspace);
+  const nl2k::slots::Key key = nl2k::slots::next_key();
   const FwdPlan p = plan_forward(B, C, nl2k::aligned16(logits));
   const dim3 grid(p.blocks);
   if (p.cached && B > 0) {
@@ -387,10 +418,10 @@ int softmax_ce_forward_f32(const float* logits, const int64_t* labels, float* lo
   do {                                                                                         \
     if (C / 4 == (TPR) * (V))                                                                  \
       hipLaunchKernelGGL((sce_fwd_kernel<TPR, V, true>), grid, dim3(kBlock), 0, stream, logits, \
-                         labels, lse, partial, B, (int)C);                                     \
+                         labels, lse, slots, key, loss, B, (int)C);                            \
     else                                                                                       \
       hipLaunchKernelGGL((sce_fwd_kernel<TPR, V, false>), grid, dim3(kBlock), 0, stream,       \
-                         logits, labels, lse, partial, B, (int)C);                             \
+                         logits, labels, lse, slots, key, loss, B, (int)C);                    \
   } while (0)
     if (p.tpr == 64 && p.v == 1) SCE_FWD(64, 1);
     else if (p.tpr == 64) SCE_FWD(64, 4);
@@ -400,12 +431,8 @@ int softmax_ce_forward_f32(const float* logits, const int64_t* labels, float* lo
 #undef SCE_FWD
   } else {
     hipLaunchKernelGGL(sce_fwd_generic_kernel, grid, dim3(kBlock), 0, stream, logits, labels, lse,
-                       partial, B, C);
+                       slots, key, loss, B, C);
   }
-  st = nl2k::check_launch(who);
-  if (st) return st;
-  hipLaunchKernelGGL(sce_finalize_kernel, dim3(1), dim3(kBlock), 0, stream, partial,
-                     (int)p.blocks, B, loss);
   return nl2k::check_launch(who);
 }
 

@@ -204,11 +204,11 @@ def test_l2norm_scale_argument_validation_without_gpu():
 def test_softmax_ce_argument_validation_without_gpu():
     lib = _load("cases.softmax_ce.op")
     fake = ctypes.c_void_p(1 << 20)  # never dereferenced: every call below fails validation
-    # one partial loss for each of at most 1024 workgroups
-    assert lib.softmax_ce_forward_workspace_bytes(8192, 1024) == 4 * 1024
-    assert lib.softmax_ce_forward_workspace_bytes(0, 1024) == 4 * 1024
+    # one 16-byte slot pair (a partial loss) for each of at most 1024 workgroups
+    assert lib.softmax_ce_forward_workspace_bytes(8192, 1024) == 16 * 1024
+    assert lib.softmax_ce_forward_workspace_bytes(0, 1024) == 16 * 1024
     assert lib.softmax_ce_forward_workspace_bytes(-1, 1024) == 0
-    need = 4 * 1024
+    need = 16 * 1024
     st = lib.softmax_ce_forward_f32(fake, fake, fake, fake, -1, 1024, fake, need, None)
     assert st == STATUS["NL2K_ERR_SHAPE"]
     st = lib.softmax_ce_forward_f32(fake, fake, fake, fake, 8, 0, fake, need, None)
@@ -217,7 +217,7 @@ def test_softmax_ce_argument_validation_without_gpu():
     assert st == STATUS["NL2K_ERR_NULL"]
     st = lib.softmax_ce_forward_f32(fake, fake, fake, fake, 8192, 1024, fake, need - 4, None)
     assert st == STATUS["NL2K_ERR_WORKSPACE"] and b"workspace" in lib.softmax_ce_last_error()
-    odd = ctypes.c_void_p((1 << 20) + 2)
+    odd = ctypes.c_void_p((1 << 20) + 4)  # 4-byte aligned; the slots need 8
     st = lib.softmax_ce_forward_f32(fake, fake, fake, fake, 8192, 1024, odd, need, None)
     assert st == STATUS["NL2K_ERR_ALIGN"]
     st = lib.softmax_ce_backward_f32(fake, fake, fake, None, fake, 8, 16, None)
