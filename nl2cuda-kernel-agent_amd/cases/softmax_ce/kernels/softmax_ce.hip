@@ -367,7 +367,7 @@ FwdPlan plan_forward(int64_t B, int64_t C, bool aligned) {
                                                             : rows_in_flight<4>();
     rows_per_step = (kBlock / p.tpr) * r;
   }
-  // B == 0 still runs one workgroup: its partial is 0 and the finalize
+  // B == 0 still runs one workgroup: its partial is 0 and its loss sum
   // writes loss = 0 / 0 = NaN (the mean of no terms, as torch's mean of an
   // empty tensor)
   p.blocks = (unsigned)std::max<int64_t>(1, std::min<int64_t>(kFwdBlocks,
