@@ -131,6 +131,35 @@ def test_softmax_ce_loss_deterministic():
     assert torch.equal(first, again)
 
 
+def test_softmax_ce_workspace_contents_never_taken():
+    """The forward's partial losses travel through nonce-tagged slots in the
+    caller's workspace: a workspace full of random bits, then the same one
+    reused by a second call on other logits, must give each call its own
+    loss (the oracle's, and bit for bit a fresh workspace's)."""
+    announce("softmax_ce forward on a random-filled, then reused, workspace")
+    from framework import capi
+    from cases.softmax_ce import op
+    lib = op._lib()
+    b, c = 8192, 1024
+    need = lib.softmax_ce_forward_workspace_bytes(b, c)
+    ws = torch.randint(-2**62, 2**62, (need // 8,), dtype=torch.int64,
+                       generator=torch.Generator().manual_seed(3)).cuda()
+    s = capi.stream_of(ws)
+    for seed in (11, 12):
+        logits, labels = _inputs(b, c, seed)
+        x, lab = logits.cuda(), labels.cuda()
+        loss = torch.empty(1, device="cuda")
+        lse = torch.empty(b, device="cuda")
+        st = lib.softmax_ce_forward_f32(capi.ptr(x), capi.ptr(lab), capi.ptr(loss), capi.ptr(lse),
+                                        b, c, capi.ptr(ws), need, s)
+        capi.check(st, lib.softmax_ce_last_error, "softmax_ce_forward")
+        fresh, _ = op.sce_forward(x, lab)
+        torch.cuda.synchronize()
+        ref_loss, _ = osc.forward_f64(logits.numpy(), labels.numpy())
+        _close("loss", loss.cpu(), np.array([ref_loss]))
+        assert torch.equal(loss, fresh.reshape(1))
+
+
 def test_softmax_ce_verify_all_reference_defaults():
     announce("softmax_ce verify_all (reference defaults [8192, 1024])")
     from cases.softmax_ce import CASE, op
