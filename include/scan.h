@@ -39,8 +39,27 @@ extern "C" {
  * chance, with probability 2^-64 per read), so a call is a single kernel
  * launch.  Calls that share a workspace must not overlap in time; calls on
  * different streams need different workspaces.  A larger workspace serves
- * smaller shapes too. */
+ * smaller shapes too.  While `stream` is being captured into a HIP graph a
+ * call enqueues a small fill kernel over the slots before the scan (replays
+ * reuse the captured nonce, so each replay must start from cleared slots);
+ * outside capture it stays one launch. */
 size_t scan_workspace_bytes(int64_t rows, int64_t D);
+
+/* Byte offset, inside the workspace of a [rows, D] call, of the uint32 trip
+ * counter (in an 8-byte word after the slots); SIZE_MAX when the shape needs
+ * no workspace or is invalid.  A chunk whose wait for its predecessors'
+ * totals exceeds a spin cap (never expected: the grid is capped at the
+ * device's resident workgroup count, but a CU-masked queue may hold fewer)
+ * adds 1 and scans with a zero carry.  The library never clears the
+ * counter: a caller that wants to detect such a trip zeroes it before the
+ * call and reads it after. */
+size_t scan_status_offset(int64_t rows, int64_t D);
+
+/* Workgroups a [rows, D] launch uses when `resident_workgroups` can be on
+ * the device at once (the library passes CU count x the occupancy the
+ * runtime reports for the kernel); -1 for invalid arguments.  Host-only
+ * planning query, no HIP call. */
+int64_t scan_launch_grid(int64_t rows, int64_t D, int64_t resident_workgroups);
 
 /* float32 -> float32 inclusive scan (scan.cu:83-95, `scan_forward`). */
 int scan_forward_f32(const float* x, float* y, int64_t rows, int64_t D,

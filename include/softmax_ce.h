@@ -39,10 +39,20 @@ extern "C" {
 #endif
 
 /* Scratch bytes softmax_ce_forward_f32 needs (8-byte aligned; a constant
- * 16384: a 16-byte slot pair for each of at most 1024 workgroups, tagged
- * with a fresh nonce per call, so no initial contents are needed); 0 for
- * invalid sizes. */
+ * 16392: a 16-byte slot pair for each of at most 1024 workgroups, tagged
+ * with a fresh nonce per call, so no initial contents are needed, then the
+ * 8-byte status word below); 0 for invalid sizes.  While `stream` is being
+ * captured into a HIP graph the forward enqueues a small fill kernel over
+ * the slots first (replays reuse the captured nonce); otherwise it is one
+ * launch. */
 size_t softmax_ce_forward_workspace_bytes(int64_t B, int64_t C);
+
+/* Byte offset in that workspace of the uint32 trip counter: workgroup 0's
+ * wait for the other workgroups' partial losses has a spin cap (never
+ * expected to fire); a trip makes the loss NaN and adds 1 here.  The
+ * library never clears it: a caller that wants to tell a trip from a NaN
+ * caused by an invalid label zeroes it before the call and reads it after. */
+size_t softmax_ce_status_offset(void);
 
 /* loss [1] and lse [B] (softmax_ce_forward.cu:52-65, `softmax_ce_forward`;
  * lse is extra: the backward reuses it instead of recomputing each row's

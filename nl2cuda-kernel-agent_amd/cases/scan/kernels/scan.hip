@@ -25,15 +25,23 @@
 //    totals of the chunks before it in its row, in a fixed order, as its
 //    carry-in.  A chunk waits only for totals, never for another chunk's
 //    carry, so there is no serial chain; sums are deterministic.  The grid
-//    is capped so that every workgroup is resident, and each workgroup walks
-//    its chunks in increasing order and publishes before it waits, so the
-//    lowest unpublished chunk can always make progress.
+//    is capped at the resident workgroup count of the current device (CU
+//    count x the occupancy the runtime reports for this kernel), and each
+//    workgroup walks its chunks in increasing order and publishes before it
+//    waits, so the lowest unpublished chunk can always make progress.  A
+//    spin cap ends a wait that never completes (a CU-masked queue can hold
+//    fewer workgroups than the device reports): the chunk then uses a zero
+//    carry and adds 1 to the workspace's trailing trip counter, which the
+//    library never clears and callers may zero and read.
 //  * Slots need no clearing, so a call is a single launch and the workspace
 //    needs no initial contents: the slots are tagged with a fresh 64-bit
 //    nonce per call (csrc/nonce_slots.h), and a reader takes only pairs this
-//    call wrote.
+//    call wrote.  While the stream is being captured into a graph the call
+//    enqueues a fill kernel over the slots first, so that replays, which
+//    reuse the captured nonce, never read an earlier replay's slots.
 //  * Reverse scans mirror the positions: logical p <-> physical D - 1 - p.
 #include <algorithm>
+#include <atomic>
 #include <cstdint>
 
 #include "../../../csrc/common.h"
@@ -52,7 +60,6 @@ constexpr int kGroups = 4;                      // 4-element groups per lane per
 constexpr int kTile = kThreads * 4 * kGroups;   // 4096 elements
 constexpr int kWaveSpan = 64 * 4 * kGroups;     // 1024 elements per wave
 constexpr int64_t kMaxChunks = 256;             // chunks per row
-constexpr int kResidentBlocks = 1024;           // 256 CUs x 4 workgroups
 constexpr unsigned kSpinLimit = 1u << 24;       // hang guard for the carry wait
 
 // ------------------------------------------------ 64-bit accumulator helpers
@@ -364,6 +371,45 @@ size_t workspace_bytes(const Plan& p) {
   return p.slots > 0 ? (size_t)p.slots * 16 + 8 : 0;
 }
 
+// Workgroups a launch uses: every chunk at once when rows are single chunks
+// (nothing waits); otherwise at most `resident`, the count that can be on the
+// device together.
+int64_t launch_grid(const Plan& p, int64_t resident) {
+  if (p.nchunk == 1) return std::min<int64_t>(p.total, INT32_MAX);
+  return std::max<int64_t>(1, std::min<int64_t>(p.total, resident));
+}
+
+// Resident workgroups of scan_rows_kernel<...> on the current device: CU
+// count x the occupancy the runtime computes for this kernel (registers, LDS
+// and launch bounds), cached per device and instantiation.
+template <typename K>
+int resident_blocks(K kernel, int* out) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cache[kMaxDevices];
+  int dev = 0;
+  int st = nl2k::check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (st) return st;
+  if (dev >= 0 && dev < kMaxDevices) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) {
+      *out = c;
+      return NL2K_SUCCESS;
+    }
+  }
+  int cus = 0, per_cu = 0;
+  st = nl2k::check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev),
+                       "hipDeviceGetAttribute(MultiprocessorCount)");
+  if (st) return st;
+  st = nl2k::check_hip(
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, 0),
+      "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+  if (st) return st;
+  const int n = std::max(1, cus) * std::max(1, per_cu);
+  if (dev >= 0 && dev < kMaxDevices) cache[dev].store(n, std::memory_order_relaxed);
+  *out = n;
+  return NL2K_SUCCESS;
+}
+
 
 int validate(int64_t rows, int64_t D, const char* who) {
   if (rows < 0 || D < 1)
@@ -398,17 +444,20 @@ int run(const In* x, Out* y, int64_t rows, int64_t D, void* workspace, size_t ws
     key = nl2k::slots::next_key();
   }
   const bool vec = D % 4 == 0 && nl2k::aligned16(x) && nl2k::aligned16(y);
-  // Single-chunk rows never wait, so their grid is not capped.
-  const int64_t grid = p.nchunk > 1 ? std::min<int64_t>(p.total, kResidentBlocks)
-                                    : std::min<int64_t>(p.total, INT32_MAX);
-  if (vec)
-    hipLaunchKernelGGL((scan_rows_kernel<In, Out, Acc, REV, true>), dim3((unsigned)grid),
-                       dim3(kThreads), 0, stream, x, y, D, p.nchunk, p.tiles, p.total, slots,
-                       key, err);
-  else
-    hipLaunchKernelGGL((scan_rows_kernel<In, Out, Acc, REV, false>), dim3((unsigned)grid),
-                       dim3(kThreads), 0, stream, x, y, D, p.nchunk, p.tiles, p.total, slots,
-                       key, err);
+  auto* kernel = vec ? &scan_rows_kernel<In, Out, Acc, REV, true>
+                     : &scan_rows_kernel<In, Out, Acc, REV, false>;
+  int resident = 1;
+  if (p.nchunk > 1) {
+    st = resident_blocks(kernel, &resident);
+    if (st) return st;
+    hipError_t qe = hipSuccess;
+    const bool cap = nl2k::slots::capturing(stream, &qe);
+    if (qe != hipSuccess) return nl2k::check_hip(qe, "hipStreamIsCapturing");
+    if (cap) nl2k::slots::clear_async(slots, 2 * p.slots, stream);
+  }
+  const int64_t grid = launch_grid(p, resident);
+  hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream, x, y, D, p.nchunk,
+                     p.tiles, p.total, slots, key, err);
   return nl2k::check_launch(who);
 }
 
@@ -421,6 +470,18 @@ const char* scan_last_error(void) { return nl2k::error_slot().text; }
 size_t scan_workspace_bytes(int64_t rows, int64_t D) {
   if (validate(rows, D, "scan_workspace_bytes")) return 0;
   return workspace_bytes(plan(rows, D));
+}
+
+size_t scan_status_offset(int64_t rows, int64_t D) {
+  if (validate(rows, D, "scan_status_offset")) return SIZE_MAX;
+  const Plan p = plan(rows, D);
+  return p.slots > 0 ? (size_t)p.slots * 16 : SIZE_MAX;
+}
+
+int64_t scan_launch_grid(int64_t rows, int64_t D, int64_t resident_workgroups) {
+  if (validate(rows, D, "scan_launch_grid") || resident_workgroups < 1) return -1;
+  if (rows == 0) return 0;
+  return launch_grid(plan(rows, D), resident_workgroups);
 }
 
 int scan_forward_f32(const float* x, float* y, int64_t rows, int64_t D, void* workspace,

@@ -6,8 +6,13 @@ gradient; ``candidate`` and ``forward_only`` keep the dict interface.  The
 argument checks follow scan.cu:67-80 (GPU tensor, 2-D, at least one row),
 widened to any D >= 1 and to int32 input (-> int64 output, as torch.cumsum).
 There is no CPU path: without a GPU the library refuses to load.
+
+With ``NL2K_CHECK=1`` in the environment every call also zeroes the
+workspace's trip counter first and reads it after (a synchronisation), and
+raises if a chunk's wait for its predecessors hit the kernel's spin cap.
 """
 
+import ctypes
 import functools
 import os
 
@@ -19,15 +24,14 @@ from framework.loader import load_kernel
 KERNEL_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "kernels")
 LIB_NAME = "scan_hip"
 SOURCES = ["scan.hip"]
-# The chunk-completion count's result is used by one lane, after the output
-# stores; the AMDGPU atomic optimizer would broadcast it to the wave, and so
-# wait for it, before them.
-EXTRA_CUDA_CFLAGS = ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"]
+SIZE_MAX = ctypes.c_size_t(-1).value
 
 
 def bind_library(lib):
     V, I64, S = capi.c_void_p, capi.c_int64, capi.c_size_t
     capi.bind(lib, "scan_workspace_bytes", [I64, I64], S)
+    capi.bind(lib, "scan_status_offset", [I64, I64], S)
+    capi.bind(lib, "scan_launch_grid", [I64, I64, I64], I64)
     for name in ("scan_forward_f32", "scan_backward_f32", "scan_forward_i32_i64",
                  "scan_forward_i32"):
         capi.bind(lib, name, [V, V, I64, I64, V, S, V])
@@ -37,8 +41,7 @@ def bind_library(lib):
 
 @functools.lru_cache(maxsize=1)
 def _lib():
-    return bind_library(load_kernel(LIB_NAME, SOURCES, base_dir=KERNEL_DIR,
-                                    extra_cuda_cflags=EXTRA_CUDA_CFLAGS))
+    return bind_library(load_kernel(LIB_NAME, SOURCES, base_dir=KERNEL_DIR))
 
 
 def _check(x, what, dtypes):
@@ -70,10 +73,20 @@ def _call(fn_name, x, out_dtype, what):
     y = torch.empty((rows, d), dtype=out_dtype, device=x.device)
     ws_bytes = lib.scan_workspace_bytes(rows, d)
     ws = _workspace(x.device, capi.stream_of(x), ws_bytes)
+    status = None
+    if capi.checking() and not torch.cuda.is_current_stream_capturing():
+        off = lib.scan_status_offset(rows, d)
+        if off != SIZE_MAX:
+            status = ws[off // 8:off // 8 + 1]
+            status.zero_()
     with torch.cuda.device(x.device):
         st = getattr(lib, fn_name)(capi.ptr(x), capi.ptr(y), rows, d, capi.ptr(ws),
                                    ws.numel() * 8, capi.stream_of(x))
     capi.check(st, lib.scan_last_error, what)
+    if status is not None:
+        trips = int(status.item()) & 0xFFFFFFFF
+        capi.require(trips == 0, f"{what}: {trips} chunk(s) hit the carry-wait spin cap "
+                                 "(fewer workgroups resident than the device reports)")
     return y
 
 

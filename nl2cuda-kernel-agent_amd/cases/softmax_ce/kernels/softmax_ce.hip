@@ -20,7 +20,9 @@
 //    one partial loss sum in a nonce-tagged slot pair (csrc/nonce_slots.h),
 //    and workgroup 0 waits for all of them and adds them in a fixed order,
 //    so the loss is deterministic and the forward is one launch.  Only
-//    workgroup 0 waits, on workgroups that never wait.  (A last-arriving-
+//    workgroup 0 waits, on workgroups that never wait.  Under graph capture
+//    a fill kernel clears the slots first (replays reuse the captured
+//    nonce).  (A last-arriving-
 //    workgroup scheme with a shared counter measured slower: 1024 atomics on
 //    one address serialise.)
 //  * Backward: lse saved by the forward turns the gradient into a pure
@@ -49,8 +51,10 @@ constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kFwdBlocks = 1024;  // most forward workgroups (one partial loss each)
 static_assert(kFwdBlocks % 256 == 0, "the loss sum reads kFwdBlocks / 256 slots per thread");
 // Workspace of the forward: one nonce-tagged slot pair (16 bytes) per
-// workgroup's partial loss.
-constexpr size_t kWorkspaceBytes = 16 * (size_t)kFwdBlocks;
+// workgroup's partial loss, then an 8-byte word whose low 32 bits count
+// spin-cap trips (never cleared by the library).
+constexpr size_t kStatusOffset = 16 * (size_t)kFwdBlocks;
+constexpr size_t kWorkspaceBytes = kStatusOffset + 8;
 constexpr unsigned kSpinLimit = 1u << 24;  // hang guard for workgroup 0's wait
 
 
@@ -93,7 +97,8 @@ constexpr int rows_in_flight() {
 // call (slot pairs 0 .. n-1) and writes loss = (their sum, in a fixed order)
 // / B.  Only this workgroup waits, and only for workgroups that never wait,
 // so the wait ends whatever the residency; the spin cap (never expected)
-// gives a NaN loss instead of a hang.  Thread t adds slots t + 256 j in j
+// gives a NaN loss instead of a hang and adds 1 to the trip counter that
+// follows the slots.  Thread t adds slots t + 256 j in j
 // order, then the workgroup reduction: the same additions a separate
 // one-workgroup kernel over the partials would make.
 __device__ void sum_partials(const unsigned long long* __restrict__ slots, nl2k::slots::Key key,
@@ -110,6 +115,9 @@ __device__ void sum_partials(const unsigned long long* __restrict__ slots, nl2k:
       unsigned spins = 0;
       while (!nl2k::slots::ready(w0, w1, key)) {
         if (++spins > kSpinLimit) {
+          unsigned* trips = reinterpret_cast<unsigned*>(
+              const_cast<unsigned long long*>(slots) + 2 * kFwdBlocks);
+          __hip_atomic_fetch_add(trips, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           w0 = key.m0 ^ (unsigned long long)__float_as_uint(NAN);
           break;
         }
@@ -396,6 +404,8 @@ size_t softmax_ce_forward_workspace_bytes(int64_t B, int64_t C) {
   return kWorkspaceBytes;
 }
 
+size_t softmax_ce_status_offset(void) { return kStatusOffset; }
+
 int softmax_ce_forward_f32(const float* logits, const int64_t* labels, float* loss, float* lse,
                            int64_t B, int64_t C, void* workspace, size_t workspace_bytes,
                            hipStream_t stream) {
@@ -413,6 +423,10 @@ int softmax_ce_forward_f32(const float* logits, const int64_t* labels, float* lo
   const nl2k::slots::Key key = nl2k::slots::next_key();
   const FwdPlan p = plan_forward(B, C, nl2k::aligned16(logits));
   const dim3 grid(p.blocks);
+  hipError_t qe = hipSuccess;
+  const bool cap = nl2k::slots::capturing(stream, &qe);
+  if (qe != hipSuccess) return nl2k::check_hip(qe, "hipStreamIsCapturing");
+  if (cap) nl2k::slots::clear_async(slots, 2 * (int64_t)p.blocks, stream);
   if (p.cached && B > 0) {
 #define SCE_FWD(TPR, V)                                                                        \
   do {                                                                                         \

@@ -7,6 +7,9 @@ is handed to the kernel as a one-element device tensor.  Unlike the
 reference, the forward also saves each row's log-sum-exp, so the backward
 is one streaming pass.  ``candidate`` and ``forward_only`` keep the dict
 interface.  There is no CPU path: without a GPU the library refuses to load.
+With ``NL2K_CHECK=1`` the forward also zeroes and reads back the
+workspace's trip counter (a synchronisation) and raises if workgroup 0's
+wait for the partial losses hit its spin cap.
 """
 
 import functools
@@ -25,6 +28,7 @@ SOURCES = ["softmax_ce.hip"]
 def bind_library(lib):
     V, I64, S = capi.c_void_p, capi.c_int64, capi.c_size_t
     capi.bind(lib, "softmax_ce_forward_workspace_bytes", [I64, I64], S)
+    capi.bind(lib, "softmax_ce_status_offset", [], S)
     capi.bind(lib, "softmax_ce_forward_f32", [V, V, V, V, I64, I64, V, S, V])
     capi.bind(lib, "softmax_ce_backward_f32", [V, V, V, V, V, I64, I64, V])
     capi.bind_last_error(lib, "softmax_ce_last_error")
@@ -53,12 +57,20 @@ def sce_forward(logits, labels):
     loss = torch.empty((), dtype=torch.float32, device=logits.device)
     lse = torch.empty(B, dtype=torch.float32, device=logits.device)
     ws_bytes = lib.softmax_ce_forward_workspace_bytes(B, C)
-    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=logits.device)
+    ws = torch.empty((ws_bytes + 7) // 8, dtype=torch.int64, device=logits.device)
+    status = None
+    if capi.checking() and not torch.cuda.is_current_stream_capturing():
+        off = lib.softmax_ce_status_offset() // 8
+        status = ws[off:off + 1]
+        status.zero_()
     with torch.cuda.device(logits.device):
         st = lib.softmax_ce_forward_f32(capi.ptr(logits), capi.ptr(labels), capi.ptr(loss),
                                         capi.ptr(lse), B, C, capi.ptr(ws), ws_bytes,
                                         capi.stream_of(logits))
     capi.check(st, lib.softmax_ce_last_error, "sce_forward")
+    if status is not None:
+        trips = int(status.item()) & 0xFFFFFFFF
+        capi.require(trips == 0, "sce_forward: the partial-loss wait hit its spin cap")
     return loss, lse
 
 

@@ -12,8 +12,16 @@
 // call's nonce and a zeroed one to 0, so neither passes; a pair read
 // half-written, or never-written memory, passes only by chance (probability
 // 2^-64 per read, the masks being hashes of n).
+//
+// Graph capture: a captured launch keeps the nonce it was captured with, so
+// every replay would accept the slots the previous replay left.  Callers
+// therefore check `capturing(stream)` and, while it is true, enqueue
+// `clear_kernel` over the slots ahead of the launch that uses them (a fill
+// kernel, not a memset node): each replay then starts from zeroed pairs,
+// which never pass the check.
 #pragma once
 
+#include <algorithm>
 #include <atomic>
 #include <chrono>
 #include <cstdint>
@@ -64,6 +72,41 @@ __device__ __forceinline__ bool ready(unsigned long long w0, unsigned long long 
 // The published bits of a ready pair.
 __device__ __forceinline__ unsigned long long decode(unsigned long long w0, Key key) {
   return w0 ^ key.m0;
+}
+
+// Zeroes `nwords` 64-bit words (grid-stride, 16-byte stores; w 16-byte
+// aligned).  Internal linkage: each library that includes this header gets
+// its own copy.
+static __global__ void clear_kernel(unsigned long long* __restrict__ w, int64_t nwords) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; 2 * i + 1 < nwords;
+       i += stride)
+    reinterpret_cast<ulonglong2*>(w)[i] = ulonglong2{0ull, 0ull};
+  if ((nwords & 1) && blockIdx.x == 0 && threadIdx.x == 0) w[nwords - 1] = 0ull;
+}
+
+// Whether `stream` is being captured into a HIP graph.  Returns a hipError_t
+// through `err` when the query itself fails.
+inline bool capturing(hipStream_t stream, hipError_t* err) {
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  *err = hipStreamIsCapturing(stream, &status);
+  return *err == hipSuccess && status == hipStreamCaptureStatusActive;
+}
+
+// Enqueues clear_kernel over `nwords` words of `w` (8-byte aligned) on
+// `stream`; a leading word that breaks 16-byte alignment is cleared by a
+// launch of its own.
+inline void clear_async(unsigned long long* w, int64_t nwords, hipStream_t stream) {
+  if (nwords <= 0) return;
+  if (reinterpret_cast<uintptr_t>(w) & 15u) {  // peel one word to reach 16-byte alignment
+    hipLaunchKernelGGL(clear_kernel, dim3(1), dim3(64), 0, stream, w, (int64_t)1);
+    ++w;
+    --nwords;
+    if (nwords == 0) return;
+  }
+  const int64_t pairs = (nwords + 1) / 2;
+  const unsigned blocks = (unsigned)std::min<int64_t>((pairs + 255) / 256, 1024);
+  hipLaunchKernelGGL(clear_kernel, dim3(blocks), dim3(256), 0, stream, w, nwords);
 }
 
 }  // namespace slots

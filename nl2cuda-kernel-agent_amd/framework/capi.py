@@ -8,6 +8,7 @@ the reference's TORCH_CHECK failures would have raised.
 """
 
 import ctypes
+import os
 
 import torch
 
@@ -53,3 +54,9 @@ def require(cond, msg):
     """TORCH_CHECK equivalent for the Python boundary."""
     if not cond:
         raise RuntimeError(msg)
+
+
+def checking():
+    """True when NL2K_CHECK=1: ops then also read the status words their
+    kernels leave in the workspace (a synchronisation per call)."""
+    return os.environ.get("NL2K_CHECK", "") == "1"

@@ -11,9 +11,11 @@ Precision policy (same as the reference, loader.py:6-8): no fast-math flags.
 Packed fp32 instructions are disabled (``-packed-fp32-ops``).
 
 Build policy: ``build_library`` always compiles.  ``load_kernel`` loads the
-library that is already built and compiles only when it is missing; a stale
-library (sources changed since it was built) is reported on stderr and still
-loaded, so GPU runs use exactly what was built beforehand.
+library that is already built and compiles only when it is missing.  A
+stale library (its recorded fingerprint of sources, shared headers and
+flags differs from the current one) is refused with a RuntimeError, so a
+run never measures or tests code other than the committed source; setting
+``NL2K_ALLOW_STALE=1`` loads it anyway, with a warning on stderr.
 """
 
 import ctypes
@@ -129,8 +131,11 @@ def load_library(name, sources, base_dir=None, extra_cuda_cflags=None,
     if not os.path.exists(out):
         build_library(name, sources, base, extra_cuda_cflags, extra_cflags, verbose)
     elif is_stale(name, sources, base, extra_cuda_cflags, extra_cflags):
-        print(f"[loader] warning: lib{name}.so is older than its sources; "
-              f"run __graft_entry__.build() to rebuild", file=sys.stderr)
+        msg = (f"lib{name}.so was built from other sources or flags than the ones in "
+               f"{base}; run __graft_entry__.build() to rebuild")
+        if os.environ.get("NL2K_ALLOW_STALE", "") != "1":
+            raise RuntimeError(msg + " (or set NL2K_ALLOW_STALE=1 to load it anyway)")
+        print(f"[loader] warning: {msg}", file=sys.stderr)
     return ctypes.CDLL(out)
 
 

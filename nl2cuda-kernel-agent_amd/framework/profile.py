@@ -85,7 +85,8 @@ def _short(name, width=90):
 
 
 def stats_table(d):
-    rows = list(csv.DictReader(open(_find(d, "kernel_stats.csv"))))
+    with open(_find(d, "kernel_stats.csv")) as f:
+        rows = list(csv.DictReader(f))
     out = []
     for r in rows:
         out.append({
@@ -125,7 +126,8 @@ def cmd_stats(ns, cmd):
 def counter_rows(d):
     """Per-dispatch counter readings: list of (dispatch, kernel, counter, value)."""
     path = _find(d, "counter_collection.csv")
-    rows = list(csv.DictReader(open(path)))
+    with open(path) as f:
+        rows = list(csv.DictReader(f))
     out = []
     for r in rows:
         name = r.get("Kernel_Name") or r.get("Kernel-Name") or ""
@@ -148,6 +150,37 @@ def per_dispatch(rows, counter, match):
     return acc, names
 
 
+def _median(values):
+    v = sorted(values)
+    return v[len(v) // 2]
+
+
+def calibrated_counter(krows, crows, counter, kernels, copy_bytes=COPY_BYTES):
+    """One PMC counter turned into bytes per launch.
+
+    `crows` are the readings of a plain device copy that moves `copy_bytes`
+    per launch (reads for FETCH_SIZE, writes for WRITE_SIZE): its median
+    reading per dispatch gives the bytes one counter unit stands for, and
+    each kernel's median per-dispatch reading in `krows` times that factor is
+    its bytes per launch.  Readings of one dispatch (one row per shader
+    engine / XCD instance) are summed first."""
+    copy_vals, _ = per_dispatch(crows, counter, ["copy"])
+    if not copy_vals:
+        raise RuntimeError(f"no copy-kernel dispatch with {counter} readings")
+    copy_med = _median(copy_vals.values())
+    factor = copy_bytes / copy_med  # bytes per counter unit
+    per_kernel = {}
+    for k in kernels:
+        vals, _ = per_dispatch(krows, counter, [k])
+        if not vals:
+            raise RuntimeError(f"kernel {k} has no {counter} readings")
+        med = _median(vals.values())
+        per_kernel[k] = {"dispatches": len(vals), "median_counter": med,
+                         "bytes_per_launch": med * factor}
+    return {"copy_counter_median": copy_med, "copy_dispatches": len(copy_vals),
+            "bytes_per_unit": factor, "kernels": per_kernel}
+
+
 def cmd_traffic(ns, cmd):
     kernels = [k for k in ns.kernels.split(",") if k]
     copy_cmd = [sys.executable, os.path.join(REPO, "bench.py"), "--copy-calibration"]
@@ -155,23 +188,7 @@ def cmd_traffic(ns, cmd):
     for counter in ("FETCH_SIZE", "WRITE_SIZE"):
         dk = _rocprof(["--pmc", counter], ns.raw, f"{ns.name}_{counter}", cmd, ns.limit)
         dc = _rocprof(["--pmc", counter], ns.raw, f"copy_{counter}", copy_cmd, ns.limit)
-        krows, crows = counter_rows(dk), counter_rows(dc)
-        copy_vals, _ = per_dispatch(crows, counter, ["copy"])
-        if not copy_vals:
-            raise RuntimeError(f"no copy-kernel dispatch with {counter} in {dc}")
-        cv = sorted(copy_vals.values())
-        copy_med = cv[len(cv) // 2]
-        factor = COPY_BYTES / copy_med  # bytes per counter unit
-        per_kernel = {}
-        for k in kernels:
-            vals, _ = per_dispatch(krows, counter, [k])
-            if not vals:
-                raise RuntimeError(f"kernel {k} has no {counter} readings in {dk}")
-            v = sorted(vals.values())
-            per_kernel[k] = {"dispatches": len(v), "median_counter": v[len(v) // 2],
-                             "bytes_per_launch": v[len(v) // 2] * factor}
-        res[counter] = {"copy_counter_median": copy_med, "copy_dispatches": len(cv),
-                        "bytes_per_unit": factor, "kernels": per_kernel}
+        res[counter] = calibrated_counter(counter_rows(dk), counter_rows(dc), counter, kernels)
     fetch = sum(x["bytes_per_launch"] for x in res["FETCH_SIZE"]["kernels"].values())
     write = sum(x["bytes_per_launch"] for x in res["WRITE_SIZE"]["kernels"].values())
     doc = {
@@ -186,6 +203,9 @@ def cmd_traffic(ns, cmd):
         "hbm_write_bytes_per_launch": round(write),
         "hbm_bytes_per_launch": round(fetch + write),
     }
+    if ns.algorithmic_bytes:
+        doc["algorithmic_bytes_per_launch"] = ns.algorithmic_bytes
+        doc["traffic_over_algorithmic"] = round((fetch + write) / ns.algorithmic_bytes, 3)
     os.makedirs(ns.out, exist_ok=True)
     jpath = os.path.join(ns.out, f"{ns.name}_traffic.json")
     with open(jpath, "w") as f:
@@ -202,6 +222,9 @@ def cmd_traffic(ns, cmd):
     lines += ["", f"Total HBM bytes per launch (all listed kernels): fetch "
               f"{doc['hbm_fetch_bytes_per_launch']:,} + write {doc['hbm_write_bytes_per_launch']:,} = "
               f"{doc['hbm_bytes_per_launch']:,}"]
+    if ns.algorithmic_bytes:
+        lines += ["", f"Algorithmic bytes per launch: {ns.algorithmic_bytes:,}; measured / "
+                  f"algorithmic = {doc['traffic_over_algorithmic']:.3f}"]
     with open(os.path.join(ns.out, f"{ns.name}_traffic.md"), "w") as f:
         f.write("\n".join(lines) + "\n")
     print("\n".join(lines))
@@ -211,21 +234,26 @@ def cmd_traffic(ns, cmd):
 MFMA_COUNTERS = ("MfmaUtil", "MfmaFlopsF32")
 
 
-def cmd_mfma(ns, cmd):
-    kernels = [k for k in ns.kernels.split(",") if k]
-    d = _rocprof(["--pmc"] + list(MFMA_COUNTERS), ns.raw, f"{ns.name}_mfma", cmd, ns.limit)
-    rows = counter_rows(d)
+def mfma_summary(rows, kernels):
+    """Median, min and max per dispatch of each MFMA counter, per kernel."""
     per_kernel = {}
     for k in kernels:
         entry = {}
         for counter in MFMA_COUNTERS:
             vals, _ = per_dispatch(rows, counter, [k])
             if not vals:
-                raise RuntimeError(f"kernel {k} has no {counter} readings in {d}")
+                raise RuntimeError(f"kernel {k} has no {counter} readings")
             v = sorted(vals.values())
             entry[counter] = {"dispatches": len(v), "median": v[len(v) // 2],
                               "min": v[0], "max": v[-1]}
         per_kernel[k] = entry
+    return per_kernel
+
+
+def cmd_mfma(ns, cmd):
+    kernels = [k for k in ns.kernels.split(",") if k]
+    d = _rocprof(["--pmc"] + list(MFMA_COUNTERS), ns.raw, f"{ns.name}_mfma", cmd, ns.limit)
+    per_kernel = mfma_summary(counter_rows(d), kernels)
     doc = {"name": ns.name, "kernels": kernels,
            "command": " ".join(shlex.quote(c) for c in _INVOCATION),
            "profiled": " ".join(shlex.quote(c) for c in cmd),
@@ -310,6 +338,9 @@ def main(argv=None):
         p.add_argument("--iters", type=int, default=50)
         if name in ("traffic", "mfma"):
             p.add_argument("--kernels", required=True, help="comma-separated kernel-name substrings")
+        if name == "traffic":
+            p.add_argument("--algorithmic-bytes", type=int, default=0,
+                           help="algorithmic bytes per launch of the listed kernels (for the ratio)")
     p = sub.add_parser("run-case")
     p.add_argument("--case", required=True)
     p.add_argument("--impl", default=None)

@@ -3,7 +3,7 @@
 Field-for-field the reference's Protocol (framework/protocol.py:12-27) with
 two changes required by this build's acceptance bar: atol = rtol = 1e-3
 (the reference uses 1e-2), and ``flush_bytes`` -- the size of the buffer the
-timing loop writes between timed iterations so that neither the L2 caches
+timing loop reads between timed iterations so that neither the L2 caches
 (4 MiB per XCD) nor the 256 MiB Infinity Cache (MALL) of an MI355X hold the
 operands of the next iteration.
 """

@@ -125,6 +125,32 @@ def test_scan_argument_validation_and_plan_without_gpu():
     st = lib.scan_forward_f32(fake, fake, 64, 65536, fake, need - 8, None)
     assert st == STATUS["NL2K_ERR_WORKSPACE"]
     assert lib.scan_forward_f32(fake, fake, 0, 65536, None, 0, None) == 0  # nothing to do
+    # the trip counter sits in the word after the slots
+    SIZE_MAX = ctypes.c_size_t(-1).value
+    assert lib.scan_status_offset(64, 65536) == 64 * 16 * 16
+    assert lib.scan_status_offset(2, 2**21 + 5) == 2 * 171 * 16
+    assert lib.scan_status_offset(4096, 4096) == SIZE_MAX  # single-chunk rows: no workspace
+    assert lib.scan_status_offset(-1, 4) == SIZE_MAX
+
+
+@pytest.mark.parametrize("resident", [1, 3, 64, 1024, 4096])
+def test_scan_launch_grid_never_exceeds_residency(resident):
+    """Multi-chunk rows wait on their predecessors, so their grid may not
+    exceed the resident workgroup count (a device with fewer CUs, or lower
+    occupancy, gets a smaller grid and a persistent loop); single-chunk rows
+    never wait and take one workgroup per row."""
+    lib = _load("cases.scan.op")
+    for rows, d in [(64, 65536), (128, 65536), (1, 1 << 20), (2, (1 << 21) + 5), (700, 8192)]:
+        nchunk = -(-d // 4096)
+        if nchunk > 256:
+            nchunk = -(-nchunk // -(-nchunk // 256))
+        total = rows * nchunk
+        assert lib.scan_launch_grid(rows, d, resident) == min(total, resident), (rows, d)
+    assert lib.scan_launch_grid(4096, 4096, resident) == 4096  # single chunks: uncapped
+    assert lib.scan_launch_grid(3, 100, resident) == 3
+    assert lib.scan_launch_grid(0, 65536, resident) == 0
+    assert lib.scan_launch_grid(64, 65536, 0) == -1
+    assert lib.scan_launch_grid(-1, 65536, resident) == -1
 
 
 def test_spmv_argument_validation_without_gpu():
@@ -182,6 +208,39 @@ def test_cosine_sim_argument_validation_without_gpu():
     assert st == STATUS["NL2K_ERR_WORKSPACE"]
 
 
+def test_layernorm_argument_validation_without_gpu():
+    lib = _load("cases.layernorm.op")
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: every call below fails validation
+    st = lib.layernorm_forward_f32(fake, fake, fake, fake, fake, fake, -1, 64, 1e-5, None)
+    assert st == STATUS["NL2K_ERR_SHAPE"] and b"B >= 0" in lib.layernorm_last_error()
+    st = lib.layernorm_forward_f32(fake, fake, fake, fake, fake, fake, 4, 0, 1e-5, None)
+    assert st == STATUS["NL2K_ERR_SHAPE"]
+    st = lib.layernorm_forward_f32(fake, fake, fake, fake, fake, fake, 1 << 31, 64, 1e-5, None)
+    assert st == STATUS["NL2K_ERR_OVERFLOW"]
+    st = lib.layernorm_forward_f32(fake, fake, fake, fake, fake, fake, 4, 64, -1.0, None)
+    assert st == STATUS["NL2K_ERR_VALUE"] and b"eps" in lib.layernorm_last_error()
+    st = lib.layernorm_forward_f32(fake, fake, fake, fake, fake, fake, 4, 64, float("nan"), None)
+    assert st == STATUS["NL2K_ERR_VALUE"]
+    st = lib.layernorm_forward_f32(fake, None, fake, fake, fake, fake, 4, 64, 1e-5, None)
+    assert st == STATUS["NL2K_ERR_NULL"]
+    assert lib.layernorm_forward_f32(None, None, None, None, None, None, 0, 64, 1e-5, None) == 0
+    need = lib.layernorm_backward_workspace_bytes(8192, 4096)
+    assert need > 0 and lib.layernorm_backward_workspace_bytes(-1, 4096) == 0
+    st = lib.layernorm_backward_f32(fake, fake, fake, fake, fake, fake, None, fake, 8192, 4096,
+                                    fake, need, None)
+    assert st == STATUS["NL2K_ERR_NULL"]
+    st = lib.layernorm_backward_f32(fake, fake, fake, fake, fake, fake, fake, fake, 8192, 4096,
+                                    fake, need - 4, None)
+    assert st == STATUS["NL2K_ERR_WORKSPACE"] and b"workspace" in lib.layernorm_last_error()
+    odd = ctypes.c_void_p((1 << 20) + 4)
+    st = lib.layernorm_backward_f32(fake, fake, fake, fake, fake, fake, fake, fake, 8192, 4096,
+                                    odd, need, None)
+    assert st == STATUS["NL2K_ERR_ALIGN"]
+    st = lib.layernorm_backward_f32(fake, fake, fake, fake, fake, fake, fake, fake, 8, 0,
+                                    fake, need, None)
+    assert st == STATUS["NL2K_ERR_SHAPE"]
+
+
 def test_l2norm_scale_argument_validation_without_gpu():
     lib = _load("cases.l2norm_scale.op")
     fake = ctypes.c_void_p(1 << 20)  # never dereferenced: every call below fails validation
@@ -204,11 +263,13 @@ def test_l2norm_scale_argument_validation_without_gpu():
 def test_softmax_ce_argument_validation_without_gpu():
     lib = _load("cases.softmax_ce.op")
     fake = ctypes.c_void_p(1 << 20)  # never dereferenced: every call below fails validation
-    # one 16-byte slot pair (a partial loss) for each of at most 1024 workgroups
-    assert lib.softmax_ce_forward_workspace_bytes(8192, 1024) == 16 * 1024
-    assert lib.softmax_ce_forward_workspace_bytes(0, 1024) == 16 * 1024
+    # one 16-byte slot pair (a partial loss) for each of at most 1024
+    # workgroups, then the 8-byte trip-counter word
+    assert lib.softmax_ce_forward_workspace_bytes(8192, 1024) == 16 * 1024 + 8
+    assert lib.softmax_ce_forward_workspace_bytes(0, 1024) == 16 * 1024 + 8
     assert lib.softmax_ce_forward_workspace_bytes(-1, 1024) == 0
-    need = 16 * 1024
+    assert lib.softmax_ce_status_offset() == 16 * 1024
+    need = 16 * 1024 + 8
     st = lib.softmax_ce_forward_f32(fake, fake, fake, fake, -1, 1024, fake, need, None)
     assert st == STATUS["NL2K_ERR_SHAPE"]
     st = lib.softmax_ce_forward_f32(fake, fake, fake, fake, 8, 0, fake, need, None)

@@ -72,3 +72,25 @@ def test_verify_all_catches_a_gradient_mistake():
                             device="cpu")
     assert not ok
     assert "[forward] PASS" in report and "[backward] FAIL" in report
+
+
+def test_loader_refuses_a_stale_library(tmp_path, monkeypatch):
+    """A library whose recorded fingerprint differs from its current sources
+    is refused (the GPU box must never run code other than the committed
+    source); NL2K_ALLOW_STALE=1 loads it anyway, with a warning."""
+    import pytest
+    from framework import loader
+    src = tmp_path / "k.hip"
+    src.write_text("extern \"C\" int f(void) { return 1; }\n")
+    lib = tmp_path / "libk.so"
+    lib.write_bytes(b"not a library")
+    (tmp_path / "libk.so.stamp").write_text(loader._fingerprint([str(src)], loader._flags(None, None)))
+    assert not loader.is_stale("k", ["k.hip"], str(tmp_path))
+    src.write_text("extern \"C\" int f(void) { return 2; }\n")  # source changed after the build
+    assert loader.is_stale("k", ["k.hip"], str(tmp_path))
+    monkeypatch.delenv("NL2K_ALLOW_STALE", raising=False)
+    with pytest.raises(RuntimeError, match="other sources or flags"):
+        loader.load_library("k", ["k.hip"], str(tmp_path))
+    monkeypatch.setenv("NL2K_ALLOW_STALE", "1")
+    with pytest.raises(OSError):  # gets as far as dlopen of the (fake) file
+        loader.load_library("k", ["k.hip"], str(tmp_path))

@@ -1,0 +1,93 @@
+"""Graph capture of the launches that hand values between workgroups
+through nonce-tagged slots (the long-row scan and the softmax CE forward).
+A captured launch keeps the nonce it was captured with, so the libraries
+clear the slots with a fill kernel captured ahead of it.  Each test replays
+one graph several times on new inputs, with eager calls and
+synchronisations between the replays, and checks every replay against the
+oracle and against an eager call on the same inputs."""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from oracle import scan as oscan
+from oracle import softmax_ce as osce
+
+pytestmark = pytest.mark.gpu
+
+
+def _capture(fn):
+    """Warm up on a side stream, then capture fn() into a graph."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = fn()
+    torch.cuda.synchronize()
+    return g, out
+
+
+@pytest.mark.parametrize("rows,d", [(64, 65536), (3, 100003)])
+def test_scan_graph_replays_with_new_inputs(rows, d):
+    announce(f"scan graph capture rows={rows} d={d}")
+    from cases.scan import op
+    x_static = torch.zeros(rows, d, device="cuda")
+    g, y_static = _capture(lambda: op.scan_forward(x_static))
+    for seed in range(4):
+        gen = torch.Generator().manual_seed(100 + seed)
+        x = (torch.rand(rows, d, generator=gen, dtype=torch.float64) * 2 - 1).float()
+        x_static.copy_(x.cuda())
+        g.replay()
+        torch.cuda.synchronize()
+        got = y_static.cpu().numpy().astype(np.float64)
+        ref = oscan.cumsum_f32(x.numpy()).astype(np.float64)
+        err = np.abs(got - ref)
+        print(f"  replay {seed}: max_abs={err.max():.3e}")
+        assert np.all(err <= 1e-3 + 1e-3 * np.abs(ref)), f"replay {seed}"
+        eager = op.scan_forward(x_static.clone())  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(eager, y_static), f"replay {seed} differs from the eager call"
+
+
+def test_scan_int_graph_replays_bit_exact():
+    announce("scan int32 -> int64 graph capture [64, 65536]")
+    from cases.scan import op
+    x_static = torch.zeros(64, 65536, dtype=torch.int32, device="cuda")
+    g, y_static = _capture(lambda: op.scan_forward(x_static))
+    for seed in range(3):
+        gen = torch.Generator().manual_seed(200 + seed)
+        x = torch.randint(-1000, 1001, (64, 65536), generator=gen, dtype=torch.int32)
+        x_static.copy_(x.cuda())
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(y_static.cpu().numpy(), oscan.cumsum_i64(x.numpy())), seed
+
+
+def test_softmax_ce_forward_graph_replays_with_new_inputs():
+    announce("softmax_ce forward graph capture [8192, 1024]")
+    from cases.softmax_ce import op
+    b, c = 8192, 1024
+    x_static = torch.zeros(b, c, device="cuda")
+    lab_static = torch.zeros(b, dtype=torch.int64, device="cuda")
+    g, (loss_static, lse_static) = _capture(lambda: op.sce_forward(x_static, lab_static))
+    for seed in range(4):
+        gen = torch.Generator().manual_seed(300 + seed)
+        x = torch.randn(b, c, generator=gen)
+        lab = torch.randint(0, c, (b,), generator=gen)
+        x_static.copy_(x.cuda())
+        lab_static.copy_(lab.cuda())
+        g.replay()
+        torch.cuda.synchronize()
+        rloss, rlse = osce.forward_f64(x.double().numpy(), lab.numpy())
+        got = float(loss_static.item())
+        print(f"  replay {seed}: loss={got:.6f} ref={rloss:.6f}")
+        assert abs(got - rloss) <= 1e-3 + 1e-3 * abs(rloss), f"replay {seed}"
+        assert np.allclose(lse_static.cpu().numpy(), rlse, atol=1e-3, rtol=1e-3)
+        eager, _ = op.sce_forward(x_static.clone(), lab_static.clone())
+        torch.cuda.synchronize()
+        assert torch.equal(eager, loss_static), f"replay {seed} differs from the eager call"

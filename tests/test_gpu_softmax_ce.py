@@ -26,6 +26,13 @@ from oracle import softmax_ce as osc
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(autouse=True)
+def _read_trip_counter(monkeypatch):
+    """Every forward through op.py zeroes the workspace's trip counter first
+    and reads it after, raising if workgroup 0's wait hit its spin cap."""
+    monkeypatch.setenv("NL2K_CHECK", "1")
+
+
 def _inputs(b, c, seed, scale=1.0):
     gen = torch.Generator().manual_seed(seed)
     logits = torch.randn(b, c, generator=gen) * scale

@@ -61,6 +61,16 @@ def zipf_inputs():
     return ref.make_zipf_inputs(1 << 20, 1 << 20, 1, 0, torch.int32)
 
 
+@pytest.mark.parametrize("seed", [1, 2])
+def test_spmv_zipf_other_seeds(seed):
+    """The acceptance recipe at further seeds: other row lengths, columns,
+    values, x and dy (seed 0 runs below, with determinism checks)."""
+    announce(f"spmv zipf 2^20 int32 D=1 fwd+bwd seed={seed}")
+    from cases.spmv import reference as ref
+    t = ref.make_zipf_inputs(1 << 20, 1 << 20, 1, seed, torch.int32)
+    _check(t["row_ptr"], t["col_idx"], t["vals"], t["X"], seed=seed)
+
+
 def test_spmv_zipf_baseline_int32(zipf_inputs):
     announce("spmv zipf 2^20 int32 D=1 fwd+bwd")
     t = zipf_inputs
