@@ -60,6 +60,29 @@ int rbf_backward_f32(const float* X, const float* Y, const float* dK,
                      int64_t M, int64_t D, float gamma, void* workspace,
                      size_t workspace_bytes, hipStream_t stream);
 
+/*
+ * Backward without a caller workspace and without any allocation: the same
+ * kernels and results as rbf_backward_f32 (bit for bit), with the region
+ * partials kept in a scratch array compiled into the library (64 MiB per
+ * GPU, held from the first call on that GPU until the process ends).  No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Shapes whose
+ * rbf_backward_workspace_bytes(N, M, D) exceeds
+ * rbf_backward_noalloc_max_bytes() are rejected with NL2K_ERR_WORKSPACE
+ * before any HIP call (N = M = 4096, D = 64 needs 34 MB and fits; 8192 does
+ * not).  Every call on one GPU shares that GPU's scratch, so calls that
+ * overlap in time on one GPU (different streams, or threads) race and must
+ * be serialised by the caller; a call needs no initial scratch contents.
+ */
+int rbf_backward_f32_noalloc(const float* X, const float* Y, const float* dK,
+                             const float* K, float* dX, float* dY, int64_t N,
+                             int64_t M, int64_t D, float gamma, hipStream_t stream);
+
+/* Size in bytes of that scratch array (the largest workspace the no-alloc
+ * entry point serves). */
+size_t rbf_backward_noalloc_max_bytes(void);
+
 /* Message of the most recent failure on the calling thread ("" if none). */
 const char* rbf_last_error(void);
 

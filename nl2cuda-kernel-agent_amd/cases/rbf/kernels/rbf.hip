@@ -34,6 +34,7 @@
 //  * Other feature widths and misaligned pointers use the generic kernels
 //    (direct sums over d, one thread per output entry / row).
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdint>
 
@@ -187,6 +188,93 @@ int launch_fill_zero(float* p, size_t count, hipStream_t stream) {
   return nl2k::check_launch("rbf fill");
 }
 
+// Both backward entry points: the caller's workspace, or the scratch array
+// below for rbf_backward_f32_noalloc.
+int backward_impl(const float* X, const float* Y, const float* dK, const float* K, float* dX,
+                  float* dY, int64_t N, int64_t M, int64_t D, float gamma, void* workspace,
+                  size_t workspace_bytes, hipStream_t stream, const char* who) {
+  int st = validate_sizes(N, M, D);
+  if (st) return st;
+  if (N == 0 && M == 0) return nl2k::succeed();
+  if ((N > 0 && (!X || !dX)) || (M > 0 && (!Y || !dY)))
+    return nl2k::fail(NL2K_ERR_NULL, "%s: X, Y, dX, dY must be non-null", who);
+  // Empty sums: dX = 0 when M == 0, dY = 0 when N == 0.
+  if (M == 0) return launch_fill_zero(dX, (size_t)(N * D), stream);
+  if (N == 0) return launch_fill_zero(dY, (size_t)(M * D), stream);
+  if (!dK || !K) return nl2k::fail(NL2K_ERR_NULL, "%s: dK and K must be non-null", who);
+
+  const float neg2g = -2.f * gamma;
+  const nl2k::pairwise::BwdPlan p = nl2k::pairwise::plan_backward(N, M, D, true);
+  const bool aligned = nl2k::aligned16(X) && nl2k::aligned16(Y) &&
+                       nl2k::aligned16(dX) && nl2k::aligned16(dY);
+  if (p.fast && aligned) {
+    const size_t need = p.ws_floats * sizeof(float);
+    if (workspace == nullptr || workspace_bytes < need)
+      return nl2k::fail(NL2K_ERR_WORKSPACE, "%s: workspace of %zu bytes required, got %zu", who,
+                        need, workspace ? workspace_bytes : (size_t)0);
+    if (!nl2k::aligned16(workspace))
+      return nl2k::fail(NL2K_ERR_ALIGN, "%s: workspace must be 16-byte aligned", who);
+    float* ws = static_cast<float*>(workspace);
+    const bool vec_nm = (M % 4 == 0) && nl2k::aligned16(dK) && nl2k::aligned16(K);
+    nl2k::pairwise::launch_bwd_tiles<RbfBwdOp>(p, X, Y, dK, K, ws, (int)N, (int)M, vec_nm,
+                                               nullptr, nullptr, stream);
+    st = nl2k::check_launch(who);
+    if (st) return st;
+    const int bx = (int)std::min<int64_t>((N * (kD / 4) + 255) / 256, 2048);
+    const int by = (int)std::min<int64_t>((M * (kD / 4) + 255) / 256, 2048);
+    hipLaunchKernelGGL(rbf_bwd_reduce_kernel, dim3(bx + by), dim3(256), 0, stream,
+                       ws + p.px, ws + p.rx, X, dX, (int)N, p.nRJ, ws + p.py, ws + p.ry,
+                       Y, dY, (int)M, p.nRI, bx, neg2g);
+    return nl2k::check_launch(who);
+  }
+
+  const int bx = (int)std::min<int64_t>((N * D + 255) / 256, 1 << 16);
+  hipLaunchKernelGGL(rbf_bwd_generic_kernel, dim3(bx), dim3(256), 0, stream, X, Y,
+                     dK, K, dX, N, M, M, D, neg2g, 0);
+  st = nl2k::check_launch(who);
+  if (st) return st;
+  const int by = (int)std::min<int64_t>((M * D + 255) / 256, 1 << 16);
+  hipLaunchKernelGGL(rbf_bwd_generic_kernel, dim3(by), dim3(256), 0, stream, Y, X,
+                     dK, K, dY, M, N, M, D, neg2g, 1);
+  return nl2k::check_launch(who);
+}
+
+// ------------------------------------------------ scratch for the no-alloc entry
+// rbf_backward_f32_noalloc keeps the backward's region partials here instead
+// of in a caller workspace: 64 MiB per GPU, held from the first use of the
+// library on that GPU until the process ends.  The name is a host-side
+// stand-in; kernels get the device address that hipGetSymbolAddress returns,
+// looked up once per device with that device current.
+constexpr size_t kScratchBytes = size_t(64) << 20;
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> scratch_ptr[kMaxDevices];
+
+int scratch_address(void** out, const char* who) {
+  int dev = -1;
+  int st = nl2k::check_hip(hipGetDevice(&dev), who);
+  if (st) return st;
+  if (dev < 0 || dev >= kMaxDevices)
+    return nl2k::fail(NL2K_ERR_HIP, "%s: device %d beyond the %d the library tracks", who, dev,
+                      kMaxDevices);
+  void* p = scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    st = nl2k::check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), who);
+    if (st) return st;
+    if (p == nullptr)
+      return nl2k::fail(NL2K_ERR_HIP, "%s: hipGetSymbolAddress returned a null scratch", who);
+    scratch_ptr[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return NL2K_SUCCESS;
+}
+
 }  // namespace
 
 extern "C" {
@@ -227,52 +315,30 @@ int rbf_backward_f32(const float* X, const float* Y, const float* dK,
                      const float* K, float* dX, float* dY, int64_t N,
                      int64_t M, int64_t D, float gamma, void* workspace,
                      size_t workspace_bytes, hipStream_t stream) {
+  return backward_impl(X, Y, dK, K, dX, dY, N, M, D, gamma, workspace, workspace_bytes, stream,
+                       "rbf_backward_f32");
+}
+
+size_t rbf_backward_noalloc_max_bytes(void) { return kScratchBytes; }
+
+int rbf_backward_f32_noalloc(const float* X, const float* Y, const float* dK, const float* K,
+                             float* dX, float* dY, int64_t N, int64_t M, int64_t D, float gamma,
+                             hipStream_t stream) {
+  const char* who = "rbf_backward_f32_noalloc";
   int st = validate_sizes(N, M, D);
   if (st) return st;
-  if (N == 0 && M == 0) return nl2k::succeed();
-  if ((N > 0 && (!X || !dX)) || (M > 0 && (!Y || !dY)))
-    return nl2k::fail(NL2K_ERR_NULL, "rbf_backward_f32: X, Y, dX, dY must be non-null");
-  // Empty sums: dX = 0 when M == 0, dY = 0 when N == 0.
-  if (M == 0) return launch_fill_zero(dX, (size_t)(N * D), stream);
-  if (N == 0) return launch_fill_zero(dY, (size_t)(M * D), stream);
-  if (!dK || !K)
-    return nl2k::fail(NL2K_ERR_NULL, "rbf_backward_f32: dK and K must be non-null");
-
-  const float neg2g = -2.f * gamma;
-  const nl2k::pairwise::BwdPlan p = nl2k::pairwise::plan_backward(N, M, D, true);
-  const bool aligned = nl2k::aligned16(X) && nl2k::aligned16(Y) &&
-                       nl2k::aligned16(dX) && nl2k::aligned16(dY);
-  if (p.fast && aligned) {
-    const size_t need = p.ws_floats * sizeof(float);
-    if (workspace == nullptr || workspace_bytes < need)
-      return nl2k::fail(NL2K_ERR_WORKSPACE,
-                        "rbf_backward_f32: workspace of %zu bytes required, got %zu",
-                        need, workspace ? workspace_bytes : (size_t)0);
-    if (!nl2k::aligned16(workspace))
-      return nl2k::fail(NL2K_ERR_ALIGN, "rbf_backward_f32: workspace must be 16-byte aligned");
-    float* ws = static_cast<float*>(workspace);
-    const bool vec_nm = (M % 4 == 0) && nl2k::aligned16(dK) && nl2k::aligned16(K);
-    nl2k::pairwise::launch_bwd_tiles<RbfBwdOp>(p, X, Y, dK, K, ws, (int)N, (int)M, vec_nm,
-                                               nullptr, nullptr, stream);
-    st = nl2k::check_launch("rbf_backward_f32");
+  const size_t need = nl2k::pairwise::plan_backward(N, M, D, true).ws_floats * sizeof(float);
+  if (need > kScratchBytes)
+    return nl2k::fail(NL2K_ERR_WORKSPACE,
+                      "%s: N=%lld M=%lld D=%lld needs %zu bytes of scratch; the library's static "
+                      "scratch holds %zu (use rbf_backward_f32 with a workspace)",
+                      who, (long long)N, (long long)M, (long long)D, need, kScratchBytes);
+  void* ws = nullptr;
+  if (need > 0 && N > 0 && M > 0) {
+    st = scratch_address(&ws, who);
     if (st) return st;
-    const int bx = (int)std::min<int64_t>((N * (kD / 4) + 255) / 256, 2048);
-    const int by = (int)std::min<int64_t>((M * (kD / 4) + 255) / 256, 2048);
-    hipLaunchKernelGGL(rbf_bwd_reduce_kernel, dim3(bx + by), dim3(256), 0, stream,
-                       ws + p.px, ws + p.rx, X, dX, (int)N, p.nRJ, ws + p.py, ws + p.ry,
-                       Y, dY, (int)M, p.nRI, bx, neg2g);
-    return nl2k::check_launch("rbf_backward_f32 (reduce)");
   }
-
-  const int bx = (int)std::min<int64_t>((N * D + 255) / 256, 1 << 16);
-  hipLaunchKernelGGL(rbf_bwd_generic_kernel, dim3(bx), dim3(256), 0, stream, X, Y,
-                     dK, K, dX, N, M, M, D, neg2g, 0);
-  st = nl2k::check_launch("rbf_backward_f32 (generic dX)");
-  if (st) return st;
-  const int by = (int)std::min<int64_t>((M * D + 255) / 256, 1 << 16);
-  hipLaunchKernelGGL(rbf_bwd_generic_kernel, dim3(by), dim3(256), 0, stream, Y, X,
-                     dK, K, dY, M, N, M, D, neg2g, 1);
-  return nl2k::check_launch("rbf_backward_f32 (generic dY)");
+  return backward_impl(X, Y, dK, K, dX, dY, N, M, D, gamma, ws, kScratchBytes, stream, who);
 }
 
 }  // extern "C"

@@ -28,6 +28,8 @@ def bind_library(lib):
     capi.bind(lib, "rbf_forward_f32", [V, V, V, I64, I64, I64, F, V])
     capi.bind(lib, "rbf_backward_workspace_bytes", [I64, I64, I64], S)
     capi.bind(lib, "rbf_backward_f32", [V, V, V, V, V, V, I64, I64, I64, F, V, S, V])
+    capi.bind(lib, "rbf_backward_f32_noalloc", [V, V, V, V, V, V, I64, I64, I64, F, V])
+    capi.bind(lib, "rbf_backward_noalloc_max_bytes", [], S)
     capi.bind_last_error(lib, "rbf_last_error")
     return lib
 

@@ -82,6 +82,22 @@ def test_rbf_argument_validation_without_gpu():
     assert st == STATUS["NL2K_ERR_NULL"]
 
 
+def test_rbf_noalloc_rejects_shapes_beyond_its_scratch_without_gpu():
+    """The no-alloc backward serves shapes whose workspace fits the 64 MiB
+    scratch compiled into the library; larger ones fail before any HIP call."""
+    lib = _load("cases.rbf.op")
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: every call below fails validation
+    cap = lib.rbf_backward_noalloc_max_bytes()
+    assert cap == 64 << 20
+    assert lib.rbf_backward_workspace_bytes(4096, 4096, 64) <= cap
+    assert lib.rbf_backward_workspace_bytes(8192, 8192, 64) > cap
+    st = lib.rbf_backward_f32_noalloc(fake, fake, fake, fake, fake, fake, 8192, 8192, 64, 0.5,
+                                      None)
+    assert st == STATUS["NL2K_ERR_WORKSPACE"] and b"scratch" in lib.rbf_last_error()
+    st = lib.rbf_backward_f32_noalloc(fake, fake, fake, fake, fake, fake, -1, 8, 64, 0.5, None)
+    assert st == STATUS["NL2K_ERR_SHAPE"]
+
+
 def test_rbf_workspace_plan():
     lib = _load("cases.rbf.op")
     # Per region slot: a [rows, 64] partial contraction plus a [rows] partial
