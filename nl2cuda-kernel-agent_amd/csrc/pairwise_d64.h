@@ -686,41 +686,52 @@ __global__ __launch_bounds__(768) void pair_bwd_d64_3r_kernel(
   // identical bits).
   auto x_chunk = [&](int t) { return min(t / n_jc + 1, n_ic - 1); };
 
-  // Tile 0's loads go out first, then waves 0-7 stage the region's Y rows
-  // (Yt <- Y[jbase .. jbase+RJ), transposed, lanes along j so the transposed
-  // LDS writes hit consecutive banks) while they are in flight.
+  // Tile 0's loads go out first.  The region's Y rows are staged by waves
+  // 0-7 as four 64-column chunks, transposed into Yt[d][j]: the chunk of the
+  // first walk position before the first barrier, the others (loaded now,
+  // behind it) right after it, before the barrier that ends step 0 (the
+  // first step that needs them).  Holding the first barrier for all 64 KB
+  // of Y delayed every region's first tile by about 2 us.  Thread tid < 512
+  // moves float4 f = tid + 512 k of a chunk: column f % 64 (lanes along j,
+  // so the transposed LDS writes hit consecutive banks), d-group f / 64.
   if (wave >= 8) {
     load_x(0, g_x, g_xs);
     load_stage(0, g_dk[0], g_k[0], g_ok[0]);
   }
-  constexpr int kYtPerThread = RJ * 16 / 512;
-  f32x4 yv[kYtPerThread];
-  float ys[kYtPerThread];
-  if (tid < 512) {
+  constexpr int kYc = 2;  // float4 per thread per chunk
+  f32x4 yv[JC][kYc];
+  float ys[JC][kYc];
+  auto commit_y = [&](int pc) {
 #pragma unroll
-    for (int k = 0; k < kYtPerThread; ++k) {
-      const int f = tid + 512 * k;
-      const size_t yr = (size_t)min(jbase + f % RJ, M - 1);
-      yv[k] = load4(Y + yr * kD + (f / RJ) * 4);
-      if constexpr (Op::kScale) ys[k] = sy[yr];
-    }
-#pragma unroll
-    for (int k = 0; k < kYtPerThread; ++k) {
-      const int f = tid + 512 * k;
-      const int j = f % RJ;
-      const int c = (f / RJ) * 4;
+    for (int k2 = 0; k2 < kYc; ++k2) {
+      const int f = tid + 512 * k2;
+      const int j = col_at(pc) * kTile + (f & 63);
+      const int c = (f >> 6) * 4;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         if constexpr (Op::kScale)
-          Yt[(c + u) * kYtLds + j] = yv[k][u] * ys[k];
+          Yt[(c + u) * kYtLds + j] = yv[pc][k2][u] * ys[pc][k2];
         else
-          Yt[(c + u) * kYtLds + j] = yv[k][u];
+          Yt[(c + u) * kYtLds + j] = yv[pc][k2][u];
       }
     }
+  };
+  if (tid < 512) {
+#pragma unroll
+    for (int pc = 0; pc < JC; ++pc) {
+      if (pc < n_jc) {
+#pragma unroll
+        for (int k2 = 0; k2 < kYc; ++k2) {
+          const int f = tid + 512 * k2;
+          const size_t yr = (size_t)min(jbase + col_at(pc) * kTile + (f & 63), M - 1);
+          yv[pc][k2] = load4(Y + yr * kD + (f >> 6) * 4);
+          if constexpr (Op::kScale) ys[pc][k2] = sy[yr];
+        }
+      }
+    }
+    commit_y(0);
   }
-  // Both roles pass 1 + n_steps barriers; the staging loop is unrolled by
-  // three, so the compute side pads its tile barriers up to n_steps.
-  const int n_steps = (n_tiles + 2) / 3 * 3;
+  // Both roles pass 1 + n_tiles barriers.
 
   if (wave >= 8) {
     // ------------------------------------------------------ staging waves
@@ -762,17 +773,25 @@ __global__ __launch_bounds__(768) void pair_bwd_d64_3r_kernel(
       __builtin_amdgcn_sched_barrier(0);
       __syncthreads();
     };
-    for (int t = 0; t < n_steps; t += 3) {
+    int t = 0;
+    for (; t + 3 <= n_tiles; t += 3) {
       step(t, g_dk[0], g_k[0], g_ok[0], g_dk[1], g_k[1], g_ok[1]);
       step(t + 1, g_dk[1], g_k[1], g_ok[1], g_dk[2], g_k[2], g_ok[2]);
       step(t + 2, g_dk[2], g_k[2], g_ok[2], g_dk[0], g_k[0], g_ok[0]);
     }
+    // the last n_tiles % 3 steps, on the same static stages (no padding
+    // steps: each would cost a barrier round and a reload of the last tile)
+    if (t < n_tiles) step(t, g_dk[0], g_k[0], g_ok[0], g_dk[1], g_k[1], g_ok[1]);
+    if (t + 1 < n_tiles) step(t + 1, g_dk[1], g_k[1], g_ok[1], g_dk[2], g_k[2], g_ok[2]);
     return;
   }
 
   // ------------------------------------------------------- compute waves
   const int wb = wave & 3;  // 16-row block of (W.Y)^T / 16-column block of (W^T.X)^T
   __syncthreads();
+#pragma unroll
+  for (int pc = 1; pc < JC; ++pc)
+    if (pc < n_jc) commit_y(pc);
   if (wave < 4) {
     // (W.Y)^T rows 16 wb.. of every tile, accumulated over the region's
     // columns and flushed per i-chunk (dX side).
@@ -827,7 +846,6 @@ __global__ __launch_bounds__(768) void pair_bwd_d64_3r_kernel(
         }
       }
     }
-    for (int t = n_tiles; t < n_steps; ++t) __syncthreads();
     return;
   }
 
@@ -875,8 +893,6 @@ __global__ __launch_bounds__(768) void pair_bwd_d64_3r_kernel(
       }
     }
   }
-  for (int t = n_tiles; t < n_steps; ++t) __syncthreads();
-
   const size_t slot = (size_t)ri * M;
 #pragma unroll
   for (int jc = 0; jc < JC; ++jc) {
