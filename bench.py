@@ -26,7 +26,8 @@ timed the same way (flush, HIP events, geometric mean of three repeats):
 RBF at 2048, 4096 and 8192 (fwd, bwd; five seeds each, outputs of every
 seed checked), LayerNorm [8192, 4096] (fwd, bwd), scan [64, 65536] (fp32
 fwd, bwd; int32 -> int64 fwd, bit-exact), CSR SpMV on the Zipf 2^20 matrix
-(fwd; bwd dX; bwd dvals + dX).  Each entry gives event us, GB/s, the
+(fwd; bwd dX; bwd dvals + dX), and the reference's default SpMM (M = K =
+4096, D = 64; fwd; bwd dvals + dX).  Each entry gives event us, GB/s, the
 fraction of its binding roof (fp32 MFMA for RBF, HBM otherwise), and
 max_abs / max_rel per output against the float64 oracle, plus the time of
 the reference's PyTorch CPU path for that call on this host.
@@ -384,6 +385,66 @@ def run_spmv_config(iters, warmup, cpu):
     return ents
 
 
+def run_spmm_config(iters, warmup, cpu):
+    """The reference's default SpMM (cases/spmv/config.py: M = K = 4096,
+    D = 64, 64 nonzeros per row, int64 indices as the reference requires):
+    forward, and the backward with dvals and dX (the autograd call)."""
+    import torch
+    from framework import capi
+    from cases.spmv import op, reference as ref
+    lib = op._lib()
+    dev = torch.device("cuda:0")
+    t = ref.make_inputs(0, torch.float32, "cpu")
+    M = t["row_ptr"].numel() - 1
+    K, D = t["X"].shape
+    dY = torch.randn(M, D, generator=torch.Generator().manual_seed(10_000))
+    ptr, col, vals, X = (t[k].to(dev) for k in ("row_ptr", "col_idx", "vals", "X"))
+    dYd = dY.to(dev)
+    nnz = vals.numel()
+    Y = torch.empty(M, D, device=dev)
+    dv, dX = torch.empty_like(vals), torch.empty_like(X)
+    wsb = lib.spmv_backward_workspace_bytes(M, K, D, nnz)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+    s, P, chk = capi.stream_of(X), capi.ptr, _ok(lib, "spmv_last_error")
+
+    def fwd():
+        chk(lib.spmv_forward_f32_i64(P(ptr), P(col), P(vals), P(X), P(Y), M, K, D, nnz, s))
+
+    def bwd():
+        chk(lib.spmv_backward_f32_i64(P(ptr), P(col), P(vals), P(X), P(dYd), P(dv), P(dX), M, K,
+                                      D, nnz, P(ws), wsb, s))
+
+    def bwd_dx():
+        chk(lib.spmv_backward_f32_i64(P(ptr), P(col), P(vals), P(X), P(dYd), None, P(dX), M, K,
+                                      D, nnz, P(ws), wsb, s))
+
+    fwd()
+    bwd()
+    torch.cuda.synchronize()
+    out = {"y": Y.cpu().numpy(), "dX": dX.cpu().numpy(), "dvals": dv.cpu().numpy()}
+    bwd()
+    torch.cuda.synchronize()
+    repeat = bool(torch.equal(dX.cpu(), torch.from_numpy(out["dX"])))
+    timer = Timer(dev)
+    name = f"spmm reference default M=K={M} D={D} nnz={nnz} int64"
+    base = 8 * (M + 1) + 12 * nnz
+    ents = [_entry(name, "forward", timer.us(fwd, iters, warmup), base + 4 * K * D + 4 * M * D),
+            _entry(name, "backward dvals + dX", timer.us(bwd, iters, warmup),
+                   base + 4 * M * D + 8 * K * D + 4 * nnz,
+                   extra={"dX_bitwise_repeatable": repeat}),
+            _entry(name, "backward dX", timer.us(bwd_dx, iters, warmup),
+                   base + 4 * M * D + 4 * K * D)]
+    if cpu:
+        host = {k: t[k] for k in ("row_ptr", "col_idx", "vals", "X")}
+        out["dX_only"] = out["dX"]
+        errs, ref_ms = cpu_spmv(host, dY, out)
+        ents[0]["outputs"] = {"y": errs["y"]}
+        ents[1]["outputs"] = {"dX": errs["dX"], "dvals": errs["dvals"]}
+        ents[0]["cpu_reference"] = ref_ms["fwd"]
+        ents[1]["cpu_reference"] = ref_ms["bwd"]
+    return ents
+
+
 # ------------------------------------------------------------------ CPU leg
 def errors(got, ref, atol=ATOL, rtol=RTOL):
     """max_abs, max_rel (over entries with |ref| > atol; smaller ones are
@@ -608,7 +669,7 @@ def main():
                     help="seconds of CPU work for the cpu_baseline sample (0 = skip the whole "
                          "CPU leg: no cpu_baseline, parity or per-config errors)")
     ap.add_argument("--configs", default="all",
-                    help="comma list of rbf2048,rbf4096,rbf8192,layernorm,scan,spmv, "
+                    help="comma list of rbf2048,rbf4096,rbf8192,layernorm,scan,spmv,spmm, "
                          "'all' or 'none' (headline only)")
     ap.add_argument("--config-iters", type=int, default=30,
                     help="timed calls per config entry (three repeats)")
@@ -698,7 +759,7 @@ def main():
             traffic = json.load(f).get("hbm_bytes_per_launch")
 
     # per-config entries (GPU timings; errors and CPU reference times from the CPU leg)
-    wanted = {"all": ["rbf2048", "rbf4096", "rbf8192", "layernorm", "scan", "spmv"],
+    wanted = {"all": ["rbf2048", "rbf4096", "rbf8192", "layernorm", "scan", "spmv", "spmm"],
               "none": []}.get(args.configs, [c for c in args.configs.split(",") if c])
     configs = []
     it, wu = args.config_iters, 3
@@ -716,6 +777,8 @@ def main():
             configs += run_scan_config(it, wu, cpu)
         elif c == "spmv":
             configs += run_spmv_config(it, wu, cpu)
+        elif c == "spmm":
+            configs += run_spmm_config(it, wu, cpu)
         else:
             raise SystemExit(f"bench.py: unknown config {c!r}")
 

@@ -13,8 +13,12 @@
  * 0 <= col_idx < K) cannot be checked without reading device memory; the
  * kernels clamp every index they load into range, so a malformed structure
  * gives wrong numbers, never an out-of-bounds access.  The forward and
- * dvals are deterministic; the order of the additions into each dX element
- * varies between runs (as with the reference's atomics).
+ * dvals are deterministic.  At D > 1 with K <= 16384 (the reference's
+ * default SpMM: M = K = 4096, D = 64) dX is deterministic too: a stable
+ * column-major copy of A is built in the workspace and each dX row is
+ * summed over its column's entries in position order.  At D == 1, and at
+ * D > 1 beyond 16384 columns, the order of the additions into each dX
+ * element varies between runs (as with the reference's atomics).
  *
  * Reference interface replaced: the pybind entries `spmv_forward(row_ptr,
  * col_idx, vals, X) -> Y` and `spmv_backward(row_ptr, col_idx, vals, X,
@@ -44,15 +48,29 @@ int spmv_forward_f32_i64(const int64_t* row_ptr, const int64_t* col_idx, const f
                          int64_t nnz, hipStream_t stream);
 
 /* Workspace bytes spmv_backward_f32_* needs when dX is requested (0 when
- * none is needed: D > 1, nnz == 0, or more than 16.7M columns, where dX is
- * accumulated with fp32 atomics instead).  The workspace is scratch: no
- * initial contents, nothing kept; 256-byte aligned. */
+ * none is needed: nnz == 0, D == 1 with more than 16.7M columns, or D > 1
+ * with more than 16384 columns or more than 2^31 - 1 nonzeros; dX is then
+ * accumulated with fp32 atomics).  The workspace is scratch: no initial
+ * contents, nothing kept; 256-byte aligned.  The size serves int32 and
+ * int64 indices alike.  At D > 1 the build of the column-major copy passes
+ * column totals between workgroups through nonce-tagged slots (one launch,
+ * no clearing); while `stream` is being captured into a HIP graph a small
+ * fill kernel clears those slots first. */
 size_t spmv_backward_workspace_bytes(int64_t M, int64_t K, int64_t D, int64_t nnz);
+
+/* Byte offset in that workspace of a uint32 trip counter for shapes that
+ * take the D > 1 column-major route (SIZE_MAX otherwise): a workgroup's wait
+ * for the column totals of the workgroups before it has a spin cap, never
+ * expected to fire; a trip adds 1 here and leaves dX wrong.  The library
+ * never clears it: a caller that wants to detect a trip zeroes it before
+ * the call and reads it after. */
+size_t spmv_status_offset(int64_t M, int64_t K, int64_t D, int64_t nnz);
 
 /* dvals [nnz] and dX [K, D] from dY [M, D] (spmv.cu:241-288,
  * `spmv_backward`).  Either output may be NULL to skip it; dX is fully
- * written.  At D == 1, dX = A^T dY is summed by column bucket in a
- * workspace of spmv_backward_workspace_bytes() bytes (see there). */
+ * written.  When dX is requested, the workspace must hold
+ * spmv_backward_workspace_bytes() bytes: at D == 1 dX = A^T dY is summed by
+ * column bucket there, at D > 1 it holds the column-major copy of A. */
 int spmv_backward_f32_i32(const int32_t* row_ptr, const int32_t* col_idx, const float* vals,
                           const float* X, const float* dY, float* dvals, float* dX,
                           int64_t M, int64_t K, int64_t D, int64_t nnz, void* workspace,

@@ -37,12 +37,18 @@
 //    16384 columns fall back to zero-fill plus fp32 atomics.
 //  * D > 1 (SpMM): L lanes per row (L = 4, 16 or 64), float4 columns when
 //    D % 4 == 0 and X / Y are 16-byte aligned; the lanes of a row share each
-//    (col, val) load and read the X row coalesced.  Backward: per nonzero a
-//    group reduction for dvals and per-element atomics for dX.
+//    (col, val) load and read the X row coalesced.  Backward (K <= 16384):
+//    dX = A^T dY through a stable column-major copy of A built in the
+//    workspace (chunk histograms, column offsets, an in-order scatter), then
+//    the same lane-group gather per column, with dvals from the same pass;
+//    deterministic, no atomics (the spmm_t_* kernels below).  Beyond 16384
+//    columns: per nonzero a group reduction for dvals and per-element
+//    atomics for dX.
 #include <algorithm>
 #include <cstdint>
 
 #include "../../../csrc/common.h"
+#include "../../../csrc/nonce_slots.h"
 #include "spmv.h"
 
 using nl2k::f32x4;
@@ -77,22 +83,23 @@ __device__ __forceinline__ int64_t ld_col(const I* __restrict__ col, int64_t p, 
 
 __device__ __forceinline__ int lane_count(bool pred) { return __popcll(__ballot(pred)); }
 
-// First r in [0, M] with row_ptr[r] + r >= target (wave-uniform result).
+// First r in [0, M] with row_ptr[r] + wr * r >= target (wave-uniform
+// result): wr = 1 searches the merge-path coordinate, wr = 0 row starts.
 template <typename I>
 __device__ int64_t rows_lower_bound(const I* __restrict__ ptr, int64_t M, int64_t nnz,
-                                    int64_t target, int lane) {
+                                    int64_t target, int lane, int64_t wr = 1) {
   int64_t lo = 0, hi = M;
   while (hi - lo > 63) {
     const int64_t step = (hi - lo + 63) / 64;
     const int64_t probe = min(hi, lo + (int64_t)lane * step);
-    const int c = lane_count(ld_ptr(ptr, probe, nnz) + probe < target);
+    const int c = lane_count(ld_ptr(ptr, probe, nnz) + wr * probe < target);
     const int64_t nlo = c > 0 ? min(hi, lo + (int64_t)(c - 1) * step) + 1 : lo;
     const int64_t nhi = c < 64 ? min(hi, lo + (int64_t)c * step) : hi;
     lo = min(nlo, nhi);
     hi = nhi;
   }
   const int64_t probe = min(hi, lo + lane);
-  const int c = lane_count(lo + lane <= hi && ld_ptr(ptr, probe, nnz) + probe < target);
+  const int c = lane_count(lo + lane <= hi && ld_ptr(ptr, probe, nnz) + wr * probe < target);
   return min(lo + c, M);
 }
 
@@ -728,11 +735,24 @@ __global__ __launch_bounds__(kThreads) void spmm_fwd_kernel(
   }
 }
 
+// Sum over each aligned group of L lanes (every lane of a group active).
+// L = 4 and 16 stay inside a DPP row: quad_perm [1,0,3,2] and [2,3,0,1],
+// then row_half_mirror and row_mirror; L = 64 uses cross-row shuffles.
 template <int L>
 __device__ __forceinline__ float group_sum(float v) {
+  if constexpr (L == 4 || L == 16) {
+    v += nl2k::dpp_mov<0xB1>(v);
+    v += nl2k::dpp_mov<0x4E>(v);
+    if constexpr (L == 16) {
+      v += nl2k::dpp_mov<0x141>(v);
+      v += nl2k::dpp_mov<0x140>(v);
+    }
+    return v;
+  } else {
 #pragma unroll
-  for (int off = L / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+    for (int off = L / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+  }
 }
 
 template <typename I, int L, bool VEC>
@@ -769,6 +789,361 @@ __global__ __launch_bounds__(kThreads) void spmm_bwd_kernel(
     }
     dot = group_sum<L>(dot);
     if (dvals && gl == 0) dvals[p] = dot;
+  }
+}
+
+// ------------------------------------------------ SpMM backward dX (D > 1)
+// dX = A^T dY without atomics and bitwise repeatable: a stable column-major
+// copy of A is built in the workspace (its entries of column c in
+// increasing position order), then each column gathers dY rows in that
+// order.  Positions are cut into chunks of P (whole rows: chunk w takes the
+// rows that start in [wP, (w+1)P)), one wave each.
+//  S1 spmm_t_hist_kernel:    H[w][c] = entries of column c in chunk w
+//                            (an LDS histogram, order-free integer counts).
+//  S2 spmm_t_offsets_kernel: 256 columns per workgroup; column totals, the
+//                            exclusive scan over columns (block prefix plus
+//                            the earlier blocks' totals, passed through
+//                            nonce-tagged slots and added in block order),
+//                            colptr, and H rewritten in place as each
+//                            chunk's first slot per column.
+//  S3 spmm_t_scatter_kernel: each chunk walks its rows in order and places
+//                            every entry at its column's LDS cursor, so
+//                            entries of one column land in position order
+//                            (within one 64-position step of a row, lanes
+//                            that share a column, found through LDS tags,
+//                            take slots in lane order).
+//  S4 spmm_t_gather_kernel:  L lanes per column sum vals * dY[row] over the
+//                            column's entries in that order (and, when asked
+//                            and D fits one pass, dvals[p] = dY[row] . X[c]).
+constexpr int kTransposeMaxCols = 16384;  // LDS of the chunk kernels (5 B per column)
+constexpr int64_t kTransposeChunk = 1024;  // positions per chunk, at least
+
+// Loads n values of src into LDS ints, eight loads per thread in flight at
+// a time (a plain loop waits for each load before its LDS write).
+template <typename T>
+__device__ __forceinline__ void load_to_lds(const T* __restrict__ src, int* __restrict__ dst,
+                                            int64_t n) {
+  constexpr int B = 8;
+  for (int64_t base = 0; base < n; base += (int64_t)B * kThreads) {
+    T v[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u)
+      v[u] = src[min(base + (int64_t)u * kThreads + threadIdx.x, n - 1)];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int64_t i = base + (int64_t)u * kThreads + threadIdx.x;
+      if (i < n) dst[i] = (int)v[u];
+    }
+  }
+}
+
+// Chunk w = positions [wP, (w+1)P), one workgroup each; H is int32 [w][K].
+template <typename I>
+__global__ __launch_bounds__(kThreads) void spmm_t_hist_kernel(const I* __restrict__ col,
+                                                               int* __restrict__ H, int64_t K,
+                                                               int64_t nnz, int64_t P) {
+  extern __shared__ int lds_i[];
+  const int64_t w = blockIdx.x;
+  for (int64_t c = threadIdx.x; c < K; c += kThreads) lds_i[c] = 0;
+  __syncthreads();
+  const int64_t p0 = w * P, p1 = min(nnz, p0 + P);
+  constexpr int B = 8;  // column loads in flight per thread
+  for (int64_t base = p0; base < p1; base += (int64_t)B * kThreads) {
+    I cv[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) cv[u] = col[min(base + (int64_t)u * kThreads + threadIdx.x, p1 - 1)];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int64_t c = (int64_t)cv[u];
+      if (base + (int64_t)u * kThreads + threadIdx.x < p1)
+        atomicAdd(&lds_i[c < 0 ? 0 : (c >= K ? K - 1 : c)], 1);
+    }
+  }
+  __syncthreads();
+  for (int64_t c = threadIdx.x; c < K; c += kThreads) H[w * K + c] = lds_i[c];
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_incl_scan(T v, int lane) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const T u = __shfl_up(v, off, 64);
+    if (lane >= off) v += u;
+  }
+  return v;
+}
+
+// 16 columns per workgroup, 16 chunk groups: thread (g, j) holds the counts
+// of column 16 b + j in chunks [g n/16, (g+1) n/16) in registers.  colptr[c]
+// = exclusive column prefix (earlier blocks' totals, passed through
+// nonce-tagged slots and added in block order, plus this block's); H[w][c]
+// is rewritten as chunk w's first slot in column c.
+constexpr int kOffCols = 16;
+constexpr int kOffGroups = kThreads / kOffCols;  // 16
+constexpr int kOffPer = 16;                      // chunks per group held in registers
+template <typename I>
+__global__ __launch_bounds__(kThreads) void spmm_t_offsets_kernel(
+    int* __restrict__ H, I* __restrict__ colptr, int64_t K, int64_t n_chunks, int64_t nnz,
+    unsigned long long* __restrict__ slots, nl2k::slots::Key key, unsigned* __restrict__ trips) {
+  __shared__ long long part[kOffGroups][kOffCols];
+  __shared__ long long s_prev;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = threadIdx.x % kOffCols, g = threadIdx.x / kOffCols;
+  const int64_t c = (int64_t)blockIdx.x * kOffCols + j;
+  const int64_t per = (n_chunks + kOffGroups - 1) / kOffGroups;
+  const int64_t w0 = min(n_chunks, g * per), w1 = min(n_chunks, w0 + per);
+  long long sum = 0;
+  int h[kOffPer];
+  const bool cached = per <= kOffPer;
+  if (c < K) {
+    if (cached) {
+#pragma unroll
+      for (int u = 0; u < kOffPer; ++u) h[u] = w0 + u < w1 ? H[(w0 + u) * K + c] : 0;
+#pragma unroll
+      for (int u = 0; u < kOffPer; ++u) sum += h[u];
+    } else {
+      for (int64_t w = w0; w < w1; ++w) sum += H[w * K + c];
+    }
+  }
+  part[g][j] = sum;
+  __syncthreads();
+  long long col_total = 0, before_g = 0;
+  for (int k = 0; k < kOffGroups; ++k) {
+    const long long v = part[k][j];
+    col_total += v;
+    before_g += k < g ? v : 0;
+  }
+  // exclusive prefix of the 16 column totals (one 16-lane row of wave 0)
+  __shared__ long long s_cpre[kOffCols];
+  if (wave == 0) {
+    long long ct = 0;
+    if (lane < kOffCols)
+      for (int k = 0; k < kOffGroups; ++k) ct += part[k][lane];
+    const long long incl = wave_incl_scan(ct, lane);
+    if (lane < kOffCols) s_cpre[lane] = incl - ct;
+    const long long block_total = __shfl(incl, 63, 64);
+    if (lane == 0) nl2k::slots::publish(slots, blockIdx.x, (unsigned long long)block_total, key);
+    long long prev = 0;
+    for (int base = 0; base < (int)blockIdx.x; base += 64) {
+      const int bb = base + lane;
+      long long v = 0;
+      if (bb < (int)blockIdx.x) {
+        unsigned long long x0 = nl2k::slots::load_word(slots + 2 * bb);
+        unsigned long long x1 = nl2k::slots::load_word(slots + 2 * bb + 1);
+        unsigned spins = 0;
+        while (!nl2k::slots::ready(x0, x1, key)) {
+          if (++spins > (1u << 24)) {  // never expected: report and give up
+            __hip_atomic_fetch_add(trips, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            x0 = key.m0;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+          x0 = nl2k::slots::load_word(slots + 2 * bb);
+          x1 = nl2k::slots::load_word(slots + 2 * bb + 1);
+        }
+        v = (long long)nl2k::slots::decode(x0, key);
+      }
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+      prev += v;
+    }
+    if (lane == 0) s_prev = prev;
+  }
+  __syncthreads();
+  if (c < K) {
+    const long long cbase = s_prev + s_cpre[j];
+    if (g == 0) {
+      colptr[c] = (I)min(cbase, (long long)nnz);
+      if (c == K - 1) colptr[K] = (I)min(cbase + col_total, (long long)nnz);
+    }
+    long long run = cbase + before_g;
+    if (cached) {
+#pragma unroll
+      for (int u = 0; u < kOffPer; ++u) {
+        if (w0 + u < w1) H[(w0 + u) * K + c] = (int)run;
+        run += h[u];
+      }
+    } else {
+      for (int64_t w = w0; w < w1; ++w) {
+        const int hv = H[w * K + c];
+        H[w * K + c] = (int)run;
+        run += hv;
+      }
+    }
+  }
+}
+
+// Largest r in [lo, hi] with row_ptr[r] <= p (row_ptr[lo] <= p assumed).
+template <typename I>
+__device__ __forceinline__ int64_t row_of(const I* __restrict__ ptr, int64_t lo, int64_t hi,
+                                          int64_t p, int64_t nnz) {
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) >> 1;
+    if (ld_ptr(ptr, mid, nnz) <= p) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Chunk w: every position's row (binary search between the rows holding
+// the chunk's first and last positions), then tiles of 256 positions in
+// order; within a tile the four waves take their slots one after another,
+// and within a wave lanes that share a column (found through LDS tags) take
+// consecutive slots in lane order.  So the entries of every column land in
+// position order.
+constexpr int kScatterTiles = 4;      // tiles per pass whose loads are issued together
+constexpr int kScatterRowWin = 2048;  // row starts of a chunk staged in LDS
+template <typename I>
+__global__ __launch_bounds__(kThreads) void spmm_t_scatter_kernel(
+    const I* __restrict__ ptr, const I* __restrict__ col, const float* __restrict__ vals,
+    const int* __restrict__ O, I* __restrict__ crow, I* __restrict__ cpos,
+    float* __restrict__ cval, int64_t M, int64_t K, int64_t nnz, int64_t P) {
+  extern __shared__ int lds_i[];  // K cursors, then K tag bytes
+  unsigned char* tag = reinterpret_cast<unsigned char*>(lds_i + K);
+  __shared__ long long s_rows[2];
+  __shared__ int s_win[kScatterRowWin];  // row_ptr[ra + 1 .. ra + kScatterRowWin]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t w = blockIdx.x;
+  const int64_t p0 = w * P, p1 = min(nnz, p0 + P);
+  // A pass's column and value loads go out first (clamped addresses, no
+  // branches), so their latency overlaps the cursor load and row search.
+  I craw[kScatterTiles];
+  float vv[kScatterTiles];
+  auto issue = [&](int64_t t0) {
+#pragma unroll
+    for (int k = 0; k < kScatterTiles; ++k) {
+      const int64_t qc = min(t0 + (int64_t)k * kThreads + threadIdx.x, nnz - 1);
+      craw[k] = col[qc];
+      vv[k] = vals[qc];
+    }
+  };
+  issue(p0);
+  load_to_lds(O + w * K, lds_i, K);
+  // rows holding positions p0 and p1 - 1 (the last r with row_ptr[r] <= p),
+  // one search per wave
+  if (wave < 2) {
+    const int64_t r = rows_lower_bound(ptr, M, nnz, wave == 0 ? p0 + 1 : p1, lane, 0) - 1;
+    if (lane == 0) s_rows[wave] = max((int64_t)0, min(r, M - 1));
+  }
+  __syncthreads();
+  const int64_t ra = s_rows[0], rb = max(s_rows[0], s_rows[1]);
+  // rows are found from an LDS copy of the chunk's row starts when they fit
+  const bool windowed = rb - ra <= kScatterRowWin;
+  if (windowed && rb > ra) load_to_lds(ptr + ra + 1, s_win, rb - ra);
+  __syncthreads();
+  for (int64_t t0 = p0; t0 < p1; t0 += (int64_t)kScatterTiles * kThreads) {
+    if (t0 != p0) issue(t0);
+    int cc[kScatterTiles];
+    int64_t rr[kScatterTiles];
+#pragma unroll
+    for (int k = 0; k < kScatterTiles; ++k) {
+      const int64_t q = t0 + (int64_t)k * kThreads + threadIdx.x;
+      const int64_t c = (int64_t)craw[k];
+      const int cl = (int)(c < 0 ? 0 : (c >= K ? K - 1 : c));
+      cc[k] = q < p1 ? cl : -1;
+      const int64_t qr = min(q, p1 - 1);
+      if (windowed) {  // row ra + n with s_win[n - 1] = row_ptr[ra + n] <= qr
+        int lo = 0, hi = (int)(rb - ra);
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if (s_win[mid - 1] <= qr) lo = mid;
+          else hi = mid - 1;
+        }
+        rr[k] = ra + lo;
+      } else {
+        rr[k] = row_of(ptr, ra, rb, qr, nnz);
+      }
+    }
+    // Tiles in order; within a tile the four waves take their slots one
+    // after another; within a wave lanes that share a column (found through
+    // LDS tags) take consecutive slots in lane order.
+#pragma unroll
+    for (int k = 0; k < kScatterTiles; ++k) {
+      const int64_t q = t0 + (int64_t)k * kThreads + threadIdx.x;
+      const bool act = q < p1;
+      for (int g = 0; g < kThreads / 64; ++g) {
+        if (wave == g) {
+          if (act) tag[cc[k]] = (unsigned char)lane;
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          const bool loser = act && tag[cc[k]] != (unsigned char)lane;
+          unsigned long long pending = __ballot(loser);
+          int rank = 0;
+          while (pending) {
+            const int leader = __builtin_ctzll(pending);
+            const int c = __shfl(cc[k], leader, 64);
+            const unsigned long long grp = __ballot(act && cc[k] == c);
+            if (act && cc[k] == c) rank = __popcll(grp & ((1ull << lane) - 1));
+            pending &= ~grp;
+          }
+          int base = 0;
+          if (act) base = lds_i[cc[k]];
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // every read before any add
+          if (act) {
+            atomicAdd(&lds_i[cc[k]], 1);
+            const int64_t pos = max((int64_t)0, min((int64_t)base + rank, nnz - 1));
+            crow[pos] = (I)rr[k];
+            cpos[pos] = (I)q;
+            cval[pos] = vv[k];
+          }
+        }
+        // the next wave reads the cursors this one advanced: LDS order only
+        // (a full __syncthreads would also wait for this wave's scattered
+        // global stores)
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+      }
+    }
+  }
+}
+
+template <typename I, int L, bool VEC, bool DV>
+__global__ __launch_bounds__(kThreads) void spmm_t_gather_kernel(
+    const I* __restrict__ colptr, const I* __restrict__ crow, const I* __restrict__ cpos,
+    const float* __restrict__ cval, const float* __restrict__ X, const float* __restrict__ dY,
+    float* __restrict__ dX, float* __restrict__ dvals, int64_t M, int64_t K, int64_t D,
+    int64_t nnz) {
+  using V = Lanes<VEC>;
+  const int64_t c = (int64_t)blockIdx.x * (kThreads / L) + threadIdx.x / L;
+  const int gl = threadIdx.x % L;
+  if (c >= K) return;  // whole groups exit together (L divides 64)
+  const int64_t s = ld_ptr(colptr, c, nnz), e = max(s, ld_ptr(colptr, c + 1, nnz));
+  for (int64_t d0 = 0; d0 < D; d0 += (int64_t)L * V::W) {
+    const int64_t d = d0 + (int64_t)gl * V::W;
+    const bool active = d < D;
+    const int64_t dc = active ? d : 0;
+    typename V::T xc = V::zero();
+    if (DV) xc = V::load(X + c * D + dc);
+    typename V::T acc = V::zero();
+    // four entries per step; the last step's missing entries repeat entry
+    // e - 1 (valid addresses) and are masked out of the sums and stores
+    for (int64_t q = s; q < e; q += 4) {
+      int64_t rr[4], pp[4];
+      float vv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t qu = min(q + u, e - 1);
+        rr[u] = min(max((int64_t)crow[qu], (int64_t)0), M - 1);
+        vv[u] = cval[qu];
+        if (DV) pp[u] = min(max((int64_t)cpos[qu], (int64_t)0), nnz - 1);
+      }
+      typename V::T gs[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) gs[u] = V::load(dY + rr[u] * D + dc);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (q + u < e) acc += vv[u] * gs[u];
+      if (DV) {
+        // every lane of the group stores the (identical) group sum: a
+        // one-lane branch would hold the position loads inside it
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const float dt = group_sum<L>(active ? V::dot(gs[u], xc) : 0.f);
+          if (q + u < e) dvals[pp[u]] = dt;
+        }
+      }
+    }
+    if (active) V::store(dX + c * D + d, acc);
   }
 }
 
@@ -889,6 +1264,139 @@ BucketPlan bucket_plan(int64_t K, int64_t D, int64_t nnz) {
   return p;
 }
 
+// Stable transpose for dX at D > 1 (spmm_t_* kernels); workspace sections
+// 256-byte aligned: trip counter (8 B, first, so its offset does not depend
+// on the index type), look-back slots [n_blocks] (16 B), H [n_chunks][K]
+// (int32 counts, then first slots), colptr [K+1] (I), crow / cpos [nnz]
+// (I), cval [nnz].  Chunks of P positions, about one per CU.
+struct TransposePlan {
+  bool use = false;
+  int64_t P = 0, n_chunks = 0, n_blocks = 0;
+  size_t off_status = 0, off_slots = 0, off_H = 0, off_colptr = 0, off_crow = 0, off_cpos = 0,
+         off_cval = 0, bytes = 0;
+};
+
+TransposePlan transpose_plan(int64_t M, int64_t K, int64_t D, int64_t nnz, size_t isz) {
+  TransposePlan p;
+  if (D <= 1 || M <= 0 || nnz <= 0 || nnz > INT32_MAX || K > kTransposeMaxCols) return p;
+  p.use = true;
+  p.P = std::max<int64_t>(kTransposeChunk, nl2k::ceil_div(nnz, 256));
+  p.P = nl2k::ceil_div(p.P, kThreads) * kThreads;
+  p.n_chunks = nl2k::ceil_div(nnz, p.P);
+  while (p.n_chunks * K > (int64_t(1) << 24)) {  // keep H within 16 M entries
+    p.P *= 2;
+    p.n_chunks = nl2k::ceil_div(nnz, p.P);
+  }
+  p.n_blocks = nl2k::ceil_div(K, kOffCols);
+  p.off_status = 0;
+  size_t off = 256;
+  p.off_slots = off;
+  off += align256((size_t)p.n_blocks * 16);
+  p.off_H = off;
+  off += align256((size_t)(p.n_chunks * K) * sizeof(int));
+  p.off_colptr = off;
+  off += align256((size_t)(K + 1) * isz);
+  p.off_crow = off;
+  off += align256((size_t)nnz * isz);
+  p.off_cpos = off;
+  off += align256((size_t)nnz * isz);
+  p.off_cval = off;
+  p.bytes = off + align256((size_t)nnz * sizeof(float));
+  return p;
+}
+
+template <typename I>
+size_t workspace_bytes_for(int64_t M, int64_t K, int64_t D, int64_t nnz) {
+  if (M <= 0) return 0;
+  if (D == 1) return bucket_plan(K, D, nnz).bytes;
+  return transpose_plan(M, K, D, nnz, sizeof(I)).bytes;
+}
+
+template <typename I>
+int transpose_backward(const TransposePlan& tp, const I* ptr, const I* col, const float* vals,
+                       const float* X, const float* dY, float* dvals, float* dX, int64_t M,
+                       int64_t K, int64_t D, int64_t nnz, char* ws, hipStream_t stream,
+                       const char* who) {
+  int* H = reinterpret_cast<int*>(ws + tp.off_H);
+  I* colptr = reinterpret_cast<I*>(ws + tp.off_colptr);
+  unsigned long long* slots = reinterpret_cast<unsigned long long*>(ws + tp.off_slots);
+  unsigned* trips = reinterpret_cast<unsigned*>(ws + tp.off_status);
+  I* crow = reinterpret_cast<I*>(ws + tp.off_crow);
+  I* cpos = reinterpret_cast<I*>(ws + tp.off_cpos);
+  float* cval = reinterpret_cast<float*>(ws + tp.off_cval);
+  hipError_t qe = hipSuccess;
+  const bool cap = nl2k::slots::capturing(stream, &qe);
+  if (qe != hipSuccess) return nl2k::check_hip(qe, "hipStreamIsCapturing");
+  if (cap) nl2k::slots::clear_async(slots, 2 * tp.n_blocks, stream);
+  int st = NL2K_SUCCESS;
+  const size_t lds = (size_t)K * sizeof(int);               // histogram kernel
+  const size_t lds_s = lds + (size_t)nl2k::ceil_div(K, 4) * 4;  // cursors + tags
+  if (lds_s > (48u << 10)) {  // up to 80 KB of dynamic LDS (K <= 16384)
+    st = nl2k::check_hip(hipFuncSetAttribute((const void*)&spmm_t_hist_kernel<I>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                         "hipFuncSetAttribute");
+    if (!st)
+      st = nl2k::check_hip(hipFuncSetAttribute((const void*)&spmm_t_scatter_kernel<I>,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               (int)lds_s),
+                           "hipFuncSetAttribute");
+    if (st) return st;
+  }
+  hipLaunchKernelGGL((spmm_t_hist_kernel<I>), dim3((unsigned)tp.n_chunks), dim3(kThreads), lds,
+                     stream, col, H, K, nnz, tp.P);
+  st = nl2k::check_launch(who);
+  if (st) return st;
+  hipLaunchKernelGGL((spmm_t_offsets_kernel<I>), dim3((unsigned)tp.n_blocks), dim3(kThreads), 0,
+                     stream, H, colptr, K, tp.n_chunks, nnz, slots, nl2k::slots::next_key(),
+                     trips);
+  st = nl2k::check_launch(who);
+  if (st) return st;
+  hipLaunchKernelGGL((spmm_t_scatter_kernel<I>), dim3((unsigned)tp.n_chunks), dim3(kThreads), lds_s,
+                     stream, ptr, col, vals, H, crow, cpos, cval, M, K, nnz, tp.P);
+  st = nl2k::check_launch(who);
+  if (st) return st;
+  const bool vec = D % 4 == 0 && nl2k::aligned16(X) && nl2k::aligned16(dY) &&
+                   nl2k::aligned16(dX);
+  const int L = lanes_for(D, vec);
+  const bool dv = dvals != nullptr && D <= (int64_t)L * (vec ? 4 : 1);
+  const int64_t blocks = nl2k::ceil_div(K, kThreads / L);
+  const dim3 grid((unsigned)blocks), block(kThreads);
+#define SPMM_T(LL, VV, DVV)                                                                   \
+  hipLaunchKernelGGL((spmm_t_gather_kernel<I, LL, VV, DVV>), grid, block, 0, stream, colptr, \
+                     crow, cpos, cval, X, dY, dX, dvals, M, K, D, nnz)
+#define SPMM_T_L(VV, DVV)                     \
+  if (L == 4) SPMM_T(4, VV, DVV);             \
+  else if (L == 16) SPMM_T(16, VV, DVV);      \
+  else SPMM_T(64, VV, DVV)
+  if (vec) {
+    if (dv) { SPMM_T_L(true, true); } else { SPMM_T_L(true, false); }
+  } else {
+    if (dv) { SPMM_T_L(false, true); } else { SPMM_T_L(false, false); }
+  }
+#undef SPMM_T_L
+#undef SPMM_T
+  st = nl2k::check_launch(who);
+  if (st || dvals == nullptr || dv) return st;
+  // dvals for D beyond one gather pass: the row-wise kernel, without dX
+  const bool vr = D % 4 == 0 && nl2k::aligned16(X) && nl2k::aligned16(dY);
+  const int Lr = lanes_for(D, vr);
+  const dim3 rgrid((unsigned)nl2k::ceil_div(M, kThreads / Lr));
+#define SPMM_DV(LL, VV)                                                                        \
+  hipLaunchKernelGGL((spmm_bwd_kernel<I, LL, VV>), rgrid, block, 0, stream, ptr, col, vals, X, \
+                     dY, dvals, (float*)nullptr, M, K, D, nnz)
+  if (vr) {
+    if (Lr == 4) SPMM_DV(4, true);
+    else if (Lr == 16) SPMM_DV(16, true);
+    else SPMM_DV(64, true);
+  } else {
+    if (Lr == 4) SPMM_DV(4, false);
+    else if (Lr == 16) SPMM_DV(16, false);
+    else SPMM_DV(64, false);
+  }
+#undef SPMM_DV
+  return nl2k::check_launch(who);
+}
+
 template <typename I>
 int backward(const I* ptr, const I* col, const float* vals, const float* X, const float* dY,
              float* dvals, float* dX, int64_t M, int64_t K, int64_t D, int64_t nnz,
@@ -936,6 +1444,16 @@ int backward(const I* ptr, const I* col, const float* vals, const float* X, cons
     hipLaunchKernelGGL(spmv_bucket_sum_kernel, dim3((unsigned)bp.nb), dim3(kSumThreads), 0,
                        stream, contrib, low, meta, bp.n_tiles, bp.nb, bp.cols, K, nnz, dX);
     return nl2k::check_launch(who);
+  }
+  const TransposePlan tp = transpose_plan(M, K, D, nnz, sizeof(I));
+  if (dX && tp.use) {
+    if (!workspace || ws_bytes < tp.bytes)
+      return nl2k::fail(NL2K_ERR_WORKSPACE, "%s: workspace of %zu bytes required, got %zu", who,
+                        tp.bytes, workspace ? ws_bytes : (size_t)0);
+    if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+      return nl2k::fail(NL2K_ERR_ALIGN, "%s: workspace must be 256-byte aligned", who);
+    return transpose_backward<I>(tp, ptr, col, vals, X, dY, dvals, dX, M, K, D, nnz,
+                                 static_cast<char*>(workspace), stream, who);
   }
   if (dX) {
     const int64_t n = K * D;
@@ -996,7 +1514,14 @@ int spmv_forward_f32_i64(const int64_t* row_ptr, const int64_t* col_idx, const f
 
 size_t spmv_backward_workspace_bytes(int64_t M, int64_t K, int64_t D, int64_t nnz) {
   if (validate(M, K, D, nnz, INT64_MAX / 2, "spmv_backward_workspace_bytes")) return 0;
-  return M > 0 ? bucket_plan(K, D, nnz).bytes : 0;
+  // the int64-index layout, which also serves int32 indices
+  return workspace_bytes_for<int64_t>(M, K, D, nnz);
+}
+
+size_t spmv_status_offset(int64_t M, int64_t K, int64_t D, int64_t nnz) {
+  if (validate(M, K, D, nnz, INT64_MAX / 2, "spmv_status_offset")) return SIZE_MAX;
+  const TransposePlan tp = transpose_plan(M, K, D, nnz, sizeof(int64_t));
+  return tp.use ? tp.off_status : SIZE_MAX;
 }
 
 int spmv_backward_f32_i32(const int32_t* row_ptr, const int32_t* col_idx, const float* vals,

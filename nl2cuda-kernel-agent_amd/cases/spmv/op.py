@@ -6,9 +6,12 @@ Mirrors the reference's cases/spmv/op.py:24-57: ``_CSRSpMMFunction`` saves
 checks follow spmv.cu:167-197 (GPU tensors, fp32 values, 1-D structure of
 matching lengths, rank-2 X with positive sizes), with int32 indices accepted
 beside int64 (row_ptr and col_idx must share the type).  There is no CPU
-path: without a GPU the library refuses to load.
+path: without a GPU the library refuses to load.  With ``NL2K_CHECK=1``
+the backward also zeroes and reads back the workspace's trip counter (a
+synchronisation) on shapes that build the column-major copy of A.
 """
 
+import ctypes
 import functools
 import os
 
@@ -20,6 +23,7 @@ from framework.loader import load_kernel
 KERNEL_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "kernels")
 LIB_NAME = "spmv_hip"
 SOURCES = ["spmv.hip"]
+SIZE_MAX = ctypes.c_size_t(-1).value
 
 
 def bind_library(lib):
@@ -29,6 +33,7 @@ def bind_library(lib):
         capi.bind(lib, f"spmv_backward_f32_{t}",
                   [V, V, V, V, V, V, V, I64, I64, I64, I64, V, capi.c_size_t, V])
     capi.bind(lib, "spmv_backward_workspace_bytes", [I64, I64, I64, I64], restype=capi.c_size_t)
+    capi.bind(lib, "spmv_status_offset", [I64, I64, I64, I64], restype=capi.c_size_t)
     capi.bind_last_error(lib, "spmv_last_error")
     return lib
 
@@ -85,13 +90,22 @@ def spmv_backward(row_ptr, col_idx, vals, X, grad_Y, need_vals=True, need_X=True
     grad_vals = torch.empty_like(vals) if need_vals else None
     grad_X = torch.empty_like(X) if need_X else None
     ws_bytes = lib.spmv_backward_workspace_bytes(M, K, D, vals.numel()) if need_X else 0
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=X.device)  # scratch
+    ws = torch.empty(max(ws_bytes, 8), dtype=torch.uint8, device=X.device)  # scratch
+    status = None
+    if need_X and capi.checking() and not torch.cuda.is_current_stream_capturing():
+        off = lib.spmv_status_offset(M, K, D, vals.numel())
+        if off != SIZE_MAX:
+            status = ws[off:off + 8].view(torch.int64)
+            status.zero_()
     with torch.cuda.device(X.device):
         st = getattr(lib, f"spmv_backward_f32_{t}")(
             capi.ptr(row_ptr), capi.ptr(col_idx), capi.ptr(vals), capi.ptr(X), capi.ptr(grad_Y),
             capi.ptr(grad_vals) if need_vals else None, capi.ptr(grad_X) if need_X else None,
             M, K, D, vals.numel(), capi.ptr(ws), ws_bytes, capi.stream_of(X))
     capi.check(st, lib.spmv_last_error, "spmv_backward")
+    if status is not None:
+        trips = int(status.item()) & 0xFFFFFFFF
+        capi.require(trips == 0, "spmv_backward: a column-total wait hit its spin cap")
     return grad_vals, grad_X
 
 

@@ -1,5 +1,6 @@
 """Graph capture of the launches that hand values between workgroups
-through nonce-tagged slots (the long-row scan and the softmax CE forward).
+through nonce-tagged slots (the long-row scan, the softmax CE forward and
+the column offsets of the SpMM backward).
 A captured launch keeps the nonce it was captured with, so the libraries
 clear the slots with a fill kernel captured ahead of it.  Each test replays
 one graph several times on new inputs, with eager calls and
@@ -91,3 +92,28 @@ def test_softmax_ce_forward_graph_replays_with_new_inputs():
         eager, _ = op.sce_forward(x_static.clone(), lab_static.clone())
         torch.cuda.synchronize()
         assert torch.equal(eager, loss_static), f"replay {seed} differs from the eager call"
+
+
+def test_spmm_backward_graph_replays_with_new_inputs():
+    announce("spmm backward graph capture (reference default M=K=4096 D=64)")
+    from cases.spmv import op, reference as ref
+    from oracle import spmv as osp
+    t = ref.make_inputs(0, torch.float32, "cpu")
+    ptr, col, vals, X = (t[k].cuda() for k in ("row_ptr", "col_idx", "vals", "X"))
+    M, D = ptr.numel() - 1, X.shape[1]
+    dy_static = torch.zeros(M, D, device="cuda")
+    g, (dv_static, dx_static) = _capture(lambda: op.spmv_backward(ptr, col, vals, X, dy_static))
+    hp, hc, hv, hx = (t[k].numpy() for k in ("row_ptr", "col_idx", "vals", "X"))
+    for seed in range(3):
+        dy = torch.randn(M, D, generator=torch.Generator().manual_seed(400 + seed))
+        dy_static.copy_(dy.cuda())
+        g.replay()
+        torch.cuda.synchronize()
+        rdv, rdx = osp.backward_f64(hp, hc, hv, hx, dy.numpy())
+        for name, got, ref_ in (("dvals", dv_static, rdv), ("dX", dx_static, rdx)):
+            err = np.abs(got.cpu().double().numpy() - ref_)
+            print(f"  replay {seed} {name}: max_abs={err.max():.3e}")
+            assert np.all(err <= 1e-3 + 1e-3 * np.abs(ref_)), f"replay {seed}: {name}"
+        edv, edx = op.spmv_backward(ptr, col, vals, X, dy_static.clone())
+        torch.cuda.synchronize()
+        assert torch.equal(edx, dx_static) and torch.equal(edv, dv_static), f"replay {seed}"

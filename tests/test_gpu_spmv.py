@@ -17,6 +17,14 @@ from oracle import spmv as osp
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(autouse=True)
+def _read_trip_counter(monkeypatch):
+    """Every backward through op.py on a column-major (D > 1) route zeroes
+    the workspace's trip counter first and reads it after, raising if a
+    column-total wait hit its spin cap."""
+    monkeypatch.setenv("NL2K_CHECK", "1")
+
+
 def _close(name, got, ref, atol=1e-3, rtol=1e-3):
     got = got.detach().cpu().double().numpy()
     ref = np.asarray(ref, dtype=np.float64)
@@ -101,6 +109,31 @@ def test_spmv_zipf_int64_matches_int32(zipf_inputs):
     assert np.isclose(lhs, float((args32[2].double() * dv64.double()).sum()), rtol=1e-4)
 
 
+@pytest.mark.parametrize("idx", [torch.int64, torch.int32])
+def test_spmm_reference_default_backward_deterministic(idx):
+    """The reference's default SpMM (M = K = 4096, D = 64, 64 nonzeros per
+    row, sorted unique columns): dX = A^T dY is summed in a fixed order, so
+    two backward calls give identical dX and dvals bit for bit, and both
+    match the float64 oracle."""
+    announce(f"spmm reference default backward determinism {idx}")
+    from cases.spmv import op, reference as ref
+    t = ref.make_inputs(0, torch.float32, "cpu")
+    ptr, col, vals, X = (t[k] for k in ("row_ptr", "col_idx", "vals", "X"))
+    ptr, col = ptr.to(idx), col.to(idx)
+    M = ptr.numel() - 1
+    dY = torch.randn(M, X.shape[1], generator=torch.Generator().manual_seed(10_000))
+    args = [ptr.cuda(), col.cuda(), vals.cuda(), X.cuda()]
+    dv1, dX1 = op.spmv_backward(*args, dY.cuda())
+    dv2, dX2 = op.spmv_backward(*args, dY.cuda())
+    _, dX3 = op.spmv_backward(*args, dY.cuda(), need_vals=False)
+    torch.cuda.synchronize()
+    assert torch.equal(dX1, dX2) and torch.equal(dX1, dX3), "dX is not bitwise repeatable"
+    assert torch.equal(dv1, dv2), "dvals is not bitwise repeatable"
+    rdv, rdX = osp.backward_f64(ptr.numpy(), col.numpy(), vals.numpy(), X.numpy(), dY.numpy())
+    _close("dvals", dv1, rdv)
+    _close("dX", dX1, rdX)
+
+
 def test_spmv_verify_all_reference_defaults():
     announce("spmv verify_all (reference defaults M=K=4096 D=64 int64)")
     from cases.spmv import CASE, op
@@ -135,7 +168,8 @@ def _lens(kind, m, k, rng):
     ("one_long", 2000, 60000, 1), ("ends_only", 5000, 400, 1), ("zipf", 20000, 5000, 1),
     ("small", 4000, 1, 1), ("small", 1, 10, 1), ("small", 500, 300, 3), ("small", 500, 300, 4),
     ("zipf", 300, 200, 17), ("zipf", 300, 200, 64), ("small", 100, 100, 100),
-    ("small", 100, 50, 256), ("one_long", 64, 64, 300), ("ends_only", 700, 90, 8)])
+    ("small", 100, 50, 256), ("one_long", 64, 64, 300), ("ends_only", 700, 90, 8),
+    ("small", 300, 20000, 4), ("small", 300, 16384, 8), ("mostly_empty", 2000, 1500, 32), ("one_long", 50, 3000, 16)])
 def test_spmv_structures(kind, m, k, d):
     announce(f"spmv {kind} M={m} K={k} D={d}")
     rng = np.random.default_rng(m + k + d)
