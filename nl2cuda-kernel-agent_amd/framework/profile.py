@@ -15,6 +15,9 @@ commit next to the code:
            give bytes-per-count factors, which turn the selected kernels'
            per-dispatch readings into HBM bytes per launch.  Writes
            <out>/<name>_traffic.json and .md.
+  counters one rocprofv3 --pmc pass per --pmc group of any counters; the
+           median per dispatch of each, per selected kernel.  Writes
+           <out>/<name>_counters.json and .md.
   mfma     one rocprofv3 --pmc pass of the derived counters MfmaUtil (the
            MFMA pipes' busy cycles over all SIMDs and the GPU-active
            cycles) and MfmaFlopsF32 (fp32 MFMA flops) for the selected
@@ -181,8 +184,14 @@ def calibrated_counter(krows, crows, counter, kernels, copy_bytes=COPY_BYTES):
             "bytes_per_unit": factor, "kernels": per_kernel}
 
 
+def kernel_list(spec):
+    """Kernel-name substrings: ';'-separated when the spec has a ';' (template
+    names carry commas), else ','-separated."""
+    return [k for k in spec.split(";" if ";" in spec else ",") if k]
+
+
 def cmd_traffic(ns, cmd):
-    kernels = [k for k in ns.kernels.split(",") if k]
+    kernels = kernel_list(ns.kernels)
     copy_cmd = [sys.executable, os.path.join(REPO, "bench.py"), "--copy-calibration"]
     res = {}
     for counter in ("FETCH_SIZE", "WRITE_SIZE"):
@@ -251,7 +260,7 @@ def mfma_summary(rows, kernels):
 
 
 def cmd_mfma(ns, cmd):
-    kernels = [k for k in ns.kernels.split(",") if k]
+    kernels = kernel_list(ns.kernels)
     d = _rocprof(["--pmc"] + list(MFMA_COUNTERS), ns.raw, f"{ns.name}_mfma", cmd, ns.limit)
     per_kernel = mfma_summary(counter_rows(d), kernels)
     doc = {"name": ns.name, "kernels": kernels,
@@ -277,6 +286,54 @@ def cmd_mfma(ns, cmd):
         lines.append(f"| `{k}` | {u['dispatches']} | {u['median']:.1f} ({u['min']:.1f}-{u['max']:.1f}) | "
                      f"{fl['median']:,.0f} |")
     with open(os.path.join(ns.out, f"{ns.name}_mfma.md"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+    return 0
+
+
+def counter_summary(rows, kernels, counters):
+    """Median per dispatch of each counter, per kernel: {kernel: {counter:
+    {"dispatches", "median"}}} (counters with no reading are left out)."""
+    out = {}
+    for k in kernels:
+        entry = {}
+        for counter in counters:
+            vals, _ = per_dispatch(rows, counter, [k])
+            if vals:
+                entry[counter] = {"dispatches": len(vals), "median": _median(vals.values())}
+        out[k] = entry
+    return out
+
+
+def cmd_counters(ns, cmd):
+    """One rocprofv3 --pmc pass per --pmc group (each within the per-block
+    limits of one pass), then the per-kernel medians per dispatch."""
+    kernels = kernel_list(ns.kernels)
+    table = {k: {} for k in kernels}
+    passes = []
+    for i, group in enumerate(ns.pmc):
+        counters = group.split()
+        d = _rocprof(["--pmc"] + counters, ns.raw, f"{ns.name}_pmc{i}", cmd, ns.limit)
+        summ = counter_summary(counter_rows(d), kernels, counters)
+        for k in kernels:
+            table[k].update(summ[k])
+        passes.append(" ".join(counters))
+    doc = {"name": ns.name, "kernels": kernels,
+           "command": " ".join(shlex.quote(c) for c in _INVOCATION),
+           "profiled": " ".join(shlex.quote(c) for c in cmd), "passes": passes,
+           "per_kernel": table}
+    os.makedirs(ns.out, exist_ok=True)
+    with open(os.path.join(ns.out, f"{ns.name}_counters.json"), "w") as f:
+        json.dump(doc, f, indent=1)
+    lines = [f"# PMC counters per dispatch (median): {ns.name}", "", "Command:", "", "```",
+             doc["command"], "```", "", "One rocprofv3 pass per group:", ""]
+    lines += [f"* `rocprofv3 --pmc {p} -- {doc['profiled']}`" for p in passes]
+    for k in kernels:
+        lines += ["", f"## `{k}`", "", "| counter | dispatches | median per dispatch |",
+                  "|---|---:|---:|"]
+        for c, v in table[k].items():
+            lines.append(f"| {c} | {v['dispatches']} | {v['median']:,.1f} |")
+    with open(os.path.join(ns.out, f"{ns.name}_counters.md"), "w") as f:
         f.write("\n".join(lines) + "\n")
     print("\n".join(lines))
     return 0
@@ -327,7 +384,7 @@ def main(argv=None):
         argv, cmd = argv[:k], argv[k + 1:]
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     sub = ap.add_subparsers(dest="what", required=True)
-    for name in ("stats", "traffic", "mfma"):
+    for name in ("stats", "traffic", "mfma", "counters"):
         p = sub.add_parser(name)
         p.add_argument("--name", required=True)
         p.add_argument("--out", default=os.path.join(REPO, "profiles"))
@@ -336,8 +393,12 @@ def main(argv=None):
         p.add_argument("--case", default=None, help="profile run-case for this case instead of a command")
         p.add_argument("--mode", choices=["forward", "both"], default="both")
         p.add_argument("--iters", type=int, default=50)
-        if name in ("traffic", "mfma"):
-            p.add_argument("--kernels", required=True, help="comma-separated kernel-name substrings")
+        if name == "counters":
+            p.add_argument("--pmc", action="append", required=True,
+                           help="space-separated counters of one pass (repeat for more passes)")
+        if name in ("traffic", "mfma", "counters"):
+            p.add_argument("--kernels", required=True,
+                           help="kernel-name substrings, ','-separated (';' when names hold commas)")
         if name == "traffic":
             p.add_argument("--algorithmic-bytes", type=int, default=0,
                            help="algorithmic bytes per launch of the listed kernels (for the ratio)")
@@ -354,7 +415,8 @@ def main(argv=None):
                "--mode", ns.mode, "--iters", str(ns.iters)]
     if not cmd:
         ap.error("give a command after -- or --case")
-    return {"stats": cmd_stats, "traffic": cmd_traffic, "mfma": cmd_mfma}[ns.what](ns, cmd)
+    return {"stats": cmd_stats, "traffic": cmd_traffic, "mfma": cmd_mfma,
+            "counters": cmd_counters}[ns.what](ns, cmd)
 
 
 if __name__ == "__main__":

@@ -113,3 +113,22 @@ def test_mfma_summary_per_kernel():
     assert s["rbf_bwd_reduce"]["MfmaUtil"]["median"] == 0.0
     with pytest.raises(RuntimeError, match="no MfmaUtil"):
         profile.mfma_summary(rows, ["not_there"])
+
+
+def test_kernel_list_separators():
+    assert profile.kernel_list("rn_bwd_kernel,rn_colsum_kernel") == ["rn_bwd_kernel",
+                                                                    "rn_colsum_kernel"]
+    assert profile.kernel_list("scan_rows_kernel<float, float, double, false;x") == [
+        "scan_rows_kernel<float, float, double, false", "x"]
+
+
+def test_counter_summary_medians_and_missing_counters():
+    rows = [(1, TILE, "TCC_REQ_sum", 10.0), (1, TILE, "TCC_REQ_sum", 5.0),
+            (2, TILE, "TCC_REQ_sum", 20.0), (3, TILE, "TCC_REQ_sum", 30.0),
+            (1, TILE, "TCC_HIT_sum", 7.0), (4, REDUCE, "TCC_REQ_sum", 2.0)]
+    s = profile.counter_summary(rows, ["pair_bwd", "rbf_bwd_reduce"],
+                                ["TCC_REQ_sum", "TCC_HIT_sum", "TCC_MISS_sum"])
+    assert s["pair_bwd"]["TCC_REQ_sum"] == {"dispatches": 3, "median": 20.0}  # {15, 20, 30}
+    assert s["pair_bwd"]["TCC_HIT_sum"]["median"] == 7.0
+    assert "TCC_MISS_sum" not in s["pair_bwd"]
+    assert s["rbf_bwd_reduce"] == {"TCC_REQ_sum": {"dispatches": 1, "median": 2.0}}
