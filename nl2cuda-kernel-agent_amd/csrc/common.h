@@ -77,6 +77,22 @@ __device__ __forceinline__ void store4(float* p, f32x4 v) {
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
+// Raw buffer resource over `bytes` bytes at `base` (stride 0, gfx9 dword 3:
+// 32-bit data format).  A load through it takes a per-lane byte offset in a
+// vector register and a wave-uniform one in a scalar register, so a tile's
+// address costs no vector instructions; a lane offset at or past `bytes`
+// reads zeros.
+typedef __amdgpu_buffer_rsrc_t buffer_rsrc;
+
+__device__ __forceinline__ buffer_rsrc make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+__device__ __forceinline__ f32x4 buffer_load4(buffer_rsrc r, uint32_t lane_off, int wave_off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, lane_off, wave_off, 0));
+}
+
 // One 16x16x4 fp32 MFMA: acc[m][n] += sum_k A[m][k] * B[k][n].
 // Lane l supplies A[l%16][l/16] in `a` and B[l/16][l%16] in `b`; the result
 // element [4*(l/16)+r][l%16] lives in register r of lane l.

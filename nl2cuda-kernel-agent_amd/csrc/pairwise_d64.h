@@ -566,7 +566,16 @@ __global__ __launch_bounds__(512) void pair_bwd_d64_kernel(
 // bit-identical to pair_bwd_d64_kernel's.  The role index is read through
 // readfirstlane so the compiler sees wave-uniform branches and gives each
 // role its own live ranges (168 VGPRs, three waves per SIMD).
-template <class Op, int JC, bool kVecNM>
+// kFull (N and M multiples of 64, every byte offset of dK / K below 2^31):
+// no tile is ragged, so the staging waves load through buffer resources
+// with the tile's offset in a scalar register and a fixed per-lane offset,
+// and form W without clamps or selects.  That takes about 50 of the ~75
+// vector instructions per staging step off the SIMDs the matrix waves
+// issue on (vector ALU and MFMA issue share a SIMD), with identical bits.
+// Otherwise every tile is loaded with clamped addresses and masked
+// (float4 loads: the launcher sends scalar-load shapes to
+// pair_bwd_d64_kernel).
+template <class Op, int JC, bool kFull>
 __global__ __launch_bounds__(768) void pair_bwd_d64_3r_kernel(
     const float* X, const float* __restrict__ Y,
     const float* dK, const float* Kf,
@@ -621,34 +630,36 @@ __global__ __launch_bounds__(768) void pair_bwd_d64_3r_kernel(
   f32x4 g_dk[3][4], g_k[3][4], g_x[4];
   float g_xs;
   bool g_ok[3][4];
+  // Full-tile addressing: byte offsets of row srow, column scol of a tile
+  // (and of row xrow, column xcol of an X chunk) from the tile's corner.
+  const uint32_t lane_off = ((uint32_t)srow * (uint32_t)M + (uint32_t)scol) * 4u;
+  const uint32_t xlane_off = (uint32_t)(xrow * kD + xcol) * 4u;
+  const uint32_t nm_bytes = kFull ? (uint32_t)N * (uint32_t)M * 4u : 0u;
+  const buffer_rsrc rdk = make_rsrc(dK, nm_bytes);
+  const buffer_rsrc rkk = make_rsrc(Kf, Op::kProduct ? nm_bytes : 0u);
+  const buffer_rsrc rxx = make_rsrc(X, kFull ? (uint32_t)N * (uint32_t)kD * 4u : 0u);
   auto load_stage = [&](int t, f32x4 (&dk)[4], f32x4 (&kk)[4], bool (&ok)[4]) {
     const int pi = t / n_jc;
     const int ic = chunk_at(pi), jc = col_at(t - pi * n_jc);
     const int ib = ibase + ic * kTile;
     const int jb = jbase + jc * kTile;
+    if constexpr (kFull) {
+      const int toff = (ib * M + jb) * 4;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int gi = ib + srow + 16 * s;
-      const int gj = jb + scol;
-      const int ci = min(gi, N - 1);
-      if (kVecNM) {
+      for (int s = 0; s < 4; ++s) {
+        ok[s] = true;
+        dk[s] = buffer_load4(rdk, lane_off, toff + s * 64 * M);
+        if constexpr (Op::kProduct) kk[s] = buffer_load4(rkk, lane_off, toff + s * 64 * M);
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int gi = ib + srow + 16 * s;
+        const int gj = jb + scol;
         ok[s] = gi < N && gj < M;
-        const size_t o = (size_t)ci * M + min(gj, M - 4);
+        const size_t o = (size_t)min(gi, N - 1) * M + min(gj, M - 4);
         dk[s] = load4(dK + o);
         if constexpr (Op::kProduct) kk[s] = load4(Kf + o);
-      } else {
-        ok[s] = gi < N;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const size_t o = (size_t)ci * M + min(gj + u, M - 1);
-          const bool in = gj + u < M;
-          const float a = dK[o];
-          dk[s][u] = in ? a : 0.f;
-          if constexpr (Op::kProduct) {
-            const float b = Kf[o];
-            kk[s][u] = in ? b : 0.f;
-          }
-        }
       }
     }
   };
@@ -657,13 +668,19 @@ __global__ __launch_bounds__(768) void pair_bwd_d64_3r_kernel(
     float* dst = P[t & 1];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      if constexpr (Op::kProduct)
-        store4(&dst[(srow + 16 * s) * kLds + scol], ok[s] ? dk[s] * kk[s] : zero4());
-      else
-        store4(&dst[(srow + 16 * s) * kLds + scol], ok[s] ? dk[s] : zero4());
+      f32x4 w = dk[s];
+      if constexpr (Op::kProduct) w = w * kk[s];
+      if constexpr (!kFull) w = ok[s] ? w : zero4();
+      store4(&dst[(srow + 16 * s) * kLds + scol], w);
     }
   };
   auto load_x = [&](int pos, f32x4 (&xs)[4], float& sc) {
+    if constexpr (kFull && !Op::kScale) {
+      const int xoff = (ibase + chunk_at(pos) * kTile) * kD * 4;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) xs[s] = buffer_load4(rxx, xlane_off + 64 * s, xoff);
+      return;
+    }
     const size_t r = (size_t)min(ibase + chunk_at(pos) * kTile + xrow, N - 1);
 #pragma unroll
     for (int s = 0; s < 4; ++s) xs[s] = load4(X + r * kD + xcol + 16 * s);
@@ -958,11 +975,18 @@ void launch_bwd_tiles(const BwdPlan& p, const float* X, const float* Y, const fl
   float* Rx = ws + p.rx;
   float* Py = ws + p.py;
   float* Ry = ws + p.ry;
-  // Vector loads of the upstream tiles: the three-role kernel.  Scalar
-  // loads (M % 4 != 0 or misaligned): the eight-wave kernel, which measured
-  // faster there (its staging needs the registers the third role takes).
-  if (vec_nm)
+  // Vector loads of the upstream tiles: the three-role kernel, with
+  // full-tile buffer addressing when no tile is ragged and every byte offset
+  // fits the resource's 32-bit range.  Scalar loads (M % 4 != 0 or
+  // misaligned): the eight-wave kernel, which measured faster there (its
+  // staging needs the registers the third role takes).
+  const bool full = N % kTile == 0 && M % kTile == 0 &&
+                    (int64_t)N * M * (int64_t)sizeof(float) < ((int64_t)1 << 31);
+  if (vec_nm && full)
     hipLaunchKernelGGL((pair_bwd_d64_3r_kernel<Op, JC, true>), dim3(p.nRI * p.nRJ), dim3(768),
+                       0, stream, X, Y, dK, K, Px, Rx, Py, Ry, N, M, p.R, p.nRJ, sx, sy);
+  else if (vec_nm)
+    hipLaunchKernelGGL((pair_bwd_d64_3r_kernel<Op, JC, false>), dim3(p.nRI * p.nRJ), dim3(768),
                        0, stream, X, Y, dK, K, Px, Rx, Py, Ry, N, M, p.R, p.nRJ, sx, sy);
   else
     hipLaunchKernelGGL((pair_bwd_d64_kernel<Op, JC, false>), dim3(p.nRI * p.nRJ), dim3(512), 0,
