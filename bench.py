@@ -26,7 +26,9 @@ timed the same way (flush, HIP events, geometric mean of three repeats):
 RBF at 2048, 4096 and 8192 (fwd, bwd; five seeds each, outputs of every
 seed checked), LayerNorm [8192, 4096] (fwd, bwd), scan [64, 65536] (fp32
 fwd, bwd; int32 -> int64 fwd, bit-exact), CSR SpMV on the Zipf 2^20 matrix
-(fwd; bwd dX; bwd dvals + dX), and the reference's default SpMM (M = K =
+(fwd; bwd dX; bwd dvals + dX; and the autograd pair when vals needs a
+gradient: fwd keeping X[col], bwd dvals + dX from it), and the reference's
+default SpMM (M = K =
 4096, D = 64; fwd; bwd dvals + dX).  Each entry gives event us, GB/s, the
 fraction of its binding roof (fp32 MFMA for RBF, HBM otherwise), and
 max_abs / max_rel per output against the float64 oracle, plus the time of
@@ -360,26 +362,52 @@ def run_spmv_config(iters, warmup, cpu):
         chk(lib.spmv_backward_f32_i32(P(ptr), P(col), P(vals), P(X), P(dYd), P(dv), P(dX), M, K, 1,
                                       nnz, P(ws), wsb, s))
 
+    # The autograd pair when vals needs a gradient: the forward also keeps
+    # X[col] (nnz floats) and the backward's dvals streams it.
+    Xg = torch.empty_like(vals)
+    dv_g, dX_g = torch.empty_like(vals), torch.empty_like(X)
+
+    def fwd_keep():
+        chk(lib.spmv_forward_gather_f32_i32(P(ptr), P(col), P(vals), P(X), P(Y), P(Xg), M, K, 1,
+                                            nnz, s))
+
+    def bwd_gathered():
+        chk(lib.spmv_backward_gathered_f32_i32(P(ptr), P(col), P(vals), P(X), P(Xg), P(dYd),
+                                               P(dv_g), P(dX_g), M, K, 1, nnz, P(ws), wsb, s))
+
     fwd()
     bwd_both()
     torch.cuda.synchronize()
     out = {"y": Y.cpu().numpy(), "dX": dX.cpu().numpy(), "dvals": dv.cpu().numpy()}
     bwd_dx()
+    fwd_keep()
+    bwd_gathered()
     torch.cuda.synchronize()
     out["dX_only"] = dX.cpu().numpy()
+    out["y_keep"] = Y.cpu().numpy()
+    out["dX_g"], out["dvals_g"] = dX_g.cpu().numpy(), dv_g.cpu().numpy()
     timer = Timer(dev)
     name = f"spmv zipf 2^20 x 2^20 nnz={nnz} D=1 int32"
     base = 4 * (M + 1) + 8 * nnz
     ents = [_entry(name, "forward", timer.us(fwd, iters, warmup), base + 4 * K + 4 * M),
             _entry(name, "backward dX", timer.us(bwd_dx, iters, warmup), base + 4 * M + 4 * K),
             _entry(name, "backward dvals + dX", timer.us(bwd_both, iters, warmup),
-                   base + 4 * M + 8 * K + 4 * nnz)]
+                   base + 4 * M + 8 * K + 4 * nnz),
+            _entry(name, "forward keeping X[col]", timer.us(fwd_keep, iters, warmup),
+                   base + 4 * K + 4 * M + 4 * nnz),
+            _entry(name, "backward dvals + dX from the kept X[col]",
+                   timer.us(bwd_gathered, iters, warmup), base + 4 * M + 4 * K + 8 * nnz)]
+    ents[3]["note"] = "autograd forward when vals requires grad"
+    ents[4]["note"] = "autograd backward after ents[3]; same dvals bits as the gathering backward"
+    ents[4]["dvals_bitwise_equal"] = bool((dv_g == dv).all().item())
     if cpu:
         host = {k: t[k] for k in ("row_ptr", "col_idx", "vals", "X")}
         errs, ref_ms = cpu_spmv(host, dY, out)
         ents[0]["outputs"] = {"y": errs["y"]}
         ents[1]["outputs"] = {"dX": errs["dX_only"]}
         ents[2]["outputs"] = {"dX": errs["dX"], "dvals": errs["dvals"]}
+        ents[3]["outputs"] = {"y": errs["y_keep"]}
+        ents[4]["outputs"] = {"dX": errs["dX_g"], "dvals": errs["dvals_g"]}
         ents[0]["cpu_reference"] = ref_ms["fwd"]
         ents[2]["cpu_reference"] = ref_ms["bwd"]
     return ents
@@ -582,7 +610,9 @@ def cpu_spmv(host, dY, out):
     y = osp.forward_f64(*args)
     dvals, dX = osp.backward_f64(*args, dY.numpy())
     errs = {"y": errors(out["y"], y), "dX": errors(out["dX"], dX),
-            "dX_only": errors(out["dX_only"], dX), "dvals": errors(out["dvals"], dvals)}
+            "dX_only": errors(out["dX_only"], dX), "dvals": errors(out["dvals"], dvals),
+            "y_keep": errors(out["y_keep"], y), "dX_g": errors(out["dX_g"], dX),
+            "dvals_g": errors(out["dvals_g"], dvals)}
     rp, ci, v, X = (host[k] for k in ("row_ptr", "col_idx", "vals", "X"))
     th = torch.get_num_threads()
     fwd_ms = _median_ms(lambda: _no_grad(osp.torch_cpu_forward, rp.long(), ci.long(), v, X))

@@ -47,6 +47,22 @@ int spmv_forward_f32_i64(const int64_t* row_ptr, const int64_t* col_idx, const f
                          const float* X, float* Y, int64_t M, int64_t K, int64_t D,
                          int64_t nnz, hipStream_t stream);
 
+/* Forward that also writes Xg [nnz] = X[col_idx[p]] (D == 1 only, the
+ * column clamped into [0, K) as the forward reads it), the gathered copy
+ * spmv_backward_gathered_f32_* reads for dvals instead of gathering X again.
+ * No counterpart in the reference (spmv.cu:199-239 is the plain forward):
+ * it trades nnz * 4 bytes kept from forward to backward for the backward's
+ * random reads of X, which bound the D == 1 walk.  D != 1 returns
+ * NL2K_ERR_SHAPE before any HIP call. */
+int spmv_forward_gather_f32_i32(const int32_t* row_ptr, const int32_t* col_idx,
+                                const float* vals, const float* X, float* Y, float* Xg,
+                                int64_t M, int64_t K, int64_t D, int64_t nnz,
+                                hipStream_t stream);
+int spmv_forward_gather_f32_i64(const int64_t* row_ptr, const int64_t* col_idx,
+                                const float* vals, const float* X, float* Y, float* Xg,
+                                int64_t M, int64_t K, int64_t D, int64_t nnz,
+                                hipStream_t stream);
+
 /* Workspace bytes spmv_backward_f32_* needs when dX is requested (0 when
  * none is needed: nnz == 0, D == 1 with more than 16.7M columns, or D > 1
  * with more than 16384 columns or more than 2^31 - 1 nonzeros; dX is then
@@ -79,6 +95,24 @@ int spmv_backward_f32_i64(const int64_t* row_ptr, const int64_t* col_idx, const 
                           const float* X, const float* dY, float* dvals, float* dX,
                           int64_t M, int64_t K, int64_t D, int64_t nnz, void* workspace,
                           size_t workspace_bytes, hipStream_t stream);
+
+/* spmv_backward_f32_* with dvals taken from Xg, the copy
+ * spmv_forward_gather_f32_* wrote for the same X and structure (D == 1
+ * only): the walk then streams vals and Xg and reads no col_idx (dX is still
+ * summed by column from col_idx).  Results are bit-identical to
+ * spmv_backward_f32_*.  Same workspace; X is still required (the fp32-atomic
+ * dX route, beyond 16.7M columns, gathers as before).  No counterpart in
+ * the reference (spmv.cu:241-288 gathers X). */
+int spmv_backward_gathered_f32_i32(const int32_t* row_ptr, const int32_t* col_idx,
+                                   const float* vals, const float* X, const float* Xg,
+                                   const float* dY, float* dvals, float* dX, int64_t M,
+                                   int64_t K, int64_t D, int64_t nnz, void* workspace,
+                                   size_t workspace_bytes, hipStream_t stream);
+int spmv_backward_gathered_f32_i64(const int64_t* row_ptr, const int64_t* col_idx,
+                                   const float* vals, const float* X, const float* Xg,
+                                   const float* dY, float* dvals, float* dX, int64_t M,
+                                   int64_t K, int64_t D, int64_t nnz, void* workspace,
+                                   size_t workspace_bytes, hipStream_t stream);
 
 const char* spmv_last_error(void);
 

@@ -46,6 +46,7 @@
 //    atomics for dX.
 #include <algorithm>
 #include <cstdint>
+#include <type_traits>
 
 #include "../../../csrc/common.h"
 #include "../../../csrc/nonce_slots.h"
@@ -154,6 +155,33 @@ struct Quad<int64_t, true> {
   __device__ float val_at(int j) const { return v[j]; }
 };
 
+// Values and gathered x entries (x[col[p]], written by the forward) of
+// positions q0..q0+3, for the backward's dvals without gathers; the same
+// clamped branch-free loads as Quad.
+template <bool VEC>
+struct QuadVX {
+  float v[4], x[4];
+  __device__ void issue(const float* __restrict__ vals, const float* __restrict__ xg, int64_t q0,
+                        int64_t nnz) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t q = max((int64_t)0, min(q0 + j, nnz - 1));
+      v[j] = vals[q];
+      x[j] = xg[q];
+    }
+  }
+};
+template <>
+struct QuadVX<true> {
+  f32x4 v, x;
+  __device__ void issue(const float* __restrict__ vals, const float* __restrict__ xg, int64_t q0,
+                        int64_t nnz) {
+    const int64_t q = max((int64_t)0, min(q0, (nnz & ~(int64_t)3) - 4));
+    v = *reinterpret_cast<const f32x4*>(vals + q);
+    x = *reinterpret_cast<const f32x4*>(xg + q);
+  }
+};
+
 // Columns (clamped into [0, K)) and values of positions q0..q0+3; in[j]
 // tells whether q0 + j lies in [lo, hi); entries outside read as column 0,
 // value 0.
@@ -243,12 +271,13 @@ __device__ __forceinline__ void window_rows(const int64_t* bnd, const Walk& s, i
 }
 
 // ------------------------------------------------------------ D == 1 forward
-template <typename I, bool VEC>
+// SAVE: also write xg[p] = x[col[p]] (column clamped) for every position.
+template <typename I, bool VEC, bool SAVE>
 __device__ __forceinline__ void fwd_walk(const I* __restrict__ ptr, const I* __restrict__ col,
                                          const float* __restrict__ vals,
                                          const float* __restrict__ x, float* __restrict__ y,
-                                         int64_t K, int64_t nnz, Walk& s, int lane,
-                                         int64_t* bnd) {
+                                         float* __restrict__ xg, int64_t K, int64_t nnz, Walk& s,
+                                         int lane, int64_t* bnd) {
   float carry_val = 0.f;
   stage_window(ptr, nnz, s, lane, bnd);
   Quad<I, VEC> cur;
@@ -277,6 +306,18 @@ __device__ __forceinline__ void fwd_walk(const I* __restrict__ ptr, const I* __r
     for (int j = 0; j < 4; ++j) xv[j] = x[c[j]];
     Quad<I, VEC> nxt;  // the next step starts at step_end
     nxt.issue(col, vals, (step_end & ~(int64_t)3) + kPer * lane, nnz);
+    if constexpr (SAVE) {
+      // Streaming stores: the copy is read once, by the backward, and must
+      // not displace x from L2.
+      if (VEC && in[0] && in[3]) {
+        __builtin_nontemporal_store(f32x4{xv[0], xv[1], xv[2], xv[3]},
+                                    reinterpret_cast<f32x4*>(xg + q0));
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (in[j]) __builtin_nontemporal_store(xv[j], xg + q0 + j);
+      }
+    }
     int64_t rid[4];
     window_rows(bnd, s, q0, step_end - 1, rid);
     float pr[4];
@@ -345,11 +386,11 @@ __device__ __forceinline__ void fwd_walk(const I* __restrict__ ptr, const I* __r
   for (int64_t r = s.carry_row + 1 + lane; r < s.r1; r += 64) y[r] = 0.f;
 }
 
-template <typename I, bool VEC>
+template <typename I, bool VEC, bool SAVE>
 __global__ __launch_bounds__(kThreads) void spmv_d1_fwd_kernel(
     const I* __restrict__ ptr, const I* __restrict__ col, const float* __restrict__ vals,
-    const float* __restrict__ x, float* __restrict__ y, int64_t M, int64_t K, int64_t nnz,
-    int64_t n_waves) {
+    const float* __restrict__ x, float* __restrict__ y, float* __restrict__ xg, int64_t M,
+    int64_t K, int64_t nnz, int64_t n_waves) {
   __shared__ int64_t bnd_s[kThreads / 64][kWin];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -359,11 +400,11 @@ __global__ __launch_bounds__(kThreads) void spmv_d1_fwd_kernel(
   if (!walk_begin(ptr, M, nnz, w, n_waves, lane, s)) return;
   if constexpr (VEC) {
     if (s.b <= (nnz & ~(int64_t)3)) {
-      fwd_walk<I, true>(ptr, col, vals, x, y, K, nnz, s, lane, bnd_s[wave]);
+      fwd_walk<I, true, SAVE>(ptr, col, vals, x, y, xg, K, nnz, s, lane, bnd_s[wave]);
       return;
     }
   }
-  fwd_walk<I, false>(ptr, col, vals, x, y, K, nnz, s, lane, bnd_s[wave]);
+  fwd_walk<I, false, SAVE>(ptr, col, vals, x, y, xg, K, nnz, s, lane, bnd_s[wave]);
 }
 
 // ----------------------------------------------------------- D == 1 backward
@@ -373,16 +414,27 @@ __global__ __launch_bounds__(kThreads) void spmv_d1_fwd_kernel(
 // zeroed dx (kAtomic, the fallback).
 constexpr int kNoDx = 0, kContrib = 1, kAtomic = 2;
 
-template <typename I, bool VEC, bool DV, int MODE>
+// GX: x[col[p]] comes from xg (the forward's gathered copy) instead of a
+// gather, and col_idx is not read at all (MODE kNoDx or kContrib only).
+template <typename I, bool VEC, bool DV, int MODE, bool GX>
 __device__ __forceinline__ void bwd_walk(const I* __restrict__ ptr, const I* __restrict__ col,
                                          const float* __restrict__ vals,
                                          const float* __restrict__ x,
+                                         const float* __restrict__ xg,
                                          const float* __restrict__ dy, float* __restrict__ dvals,
                                          float* __restrict__ out, int64_t K, int64_t nnz,
                                          Walk& s, int lane, int64_t* bnd) {
+  static_assert(!GX || MODE != kAtomic, "the gathered walk does not read columns");
+  using QuadT = std::conditional_t<GX, QuadVX<VEC>, Quad<I, VEC>>;
+  auto issue = [&](QuadT& qd, int64_t q) {
+    if constexpr (GX)
+      qd.issue(vals, xg, q, nnz);
+    else
+      qd.issue(col, vals, q, nnz);
+  };
   stage_window(ptr, nnz, s, lane, bnd);
-  Quad<I, VEC> cur;
-  if (s.pos < s.b) cur.issue(col, vals, (s.pos & ~(int64_t)3) + kPer * lane, nnz);
+  QuadT cur;
+  if (s.pos < s.b) issue(cur, (s.pos & ~(int64_t)3) + kPer * lane);
   while (s.pos < s.b) {
     const int64_t base = s.pos & ~(int64_t)3;
     const int64_t want = min(base + kStep, s.b);
@@ -394,20 +446,30 @@ __device__ __forceinline__ void bwd_walk(const I* __restrict__ ptr, const I* __r
     const int64_t step_end = min(want, s.wlimit);
     const int64_t q0 = base + kPer * lane;
     int64_t c[4];
-    float v[4];
+    float v[4], xv[4];
     bool in[4];
-    quad_get(cur, K, q0, s.pos, step_end, c, v, in);
+    if constexpr (GX) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        in[j] = q0 + j >= s.pos && q0 + j < step_end;
+        v[j] = in[j] ? cur.v[j] : 0.f;
+        xv[j] = cur.x[j];
+        c[j] = 0;
+      }
+    } else {
+      quad_get(cur, K, q0, s.pos, step_end, c, v, in);
+    }
     int64_t rid[4];
     window_rows(bnd, s, q0, step_end - 1, rid);
-    float g[4], xv[4];
+    float g[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) g[j] = dy[rid[j]];
-    if constexpr (DV) {
+    if constexpr (DV && !GX) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) xv[j] = x[c[j]];
     }
-    Quad<I, VEC> nxt;
-    nxt.issue(col, vals, (step_end & ~(int64_t)3) + kPer * lane, nnz);
+    QuadT nxt;
+    issue(nxt, (step_end & ~(int64_t)3) + kPer * lane);
     const bool full = in[0] && in[3];
     if constexpr (DV) {
       if (VEC && full) {
@@ -443,11 +505,12 @@ __device__ __forceinline__ void bwd_walk(const I* __restrict__ ptr, const I* __r
 }
 
 // `out` is the contribution array (kContrib) or dx (kAtomic).
-template <typename I, bool VEC, bool DV, int MODE>
+template <typename I, bool VEC, bool DV, int MODE, bool GX>
 __global__ __launch_bounds__(kThreads) void spmv_d1_bwd_kernel(
     const I* __restrict__ ptr, const I* __restrict__ col, const float* __restrict__ vals,
-    const float* __restrict__ x, const float* __restrict__ dy, float* __restrict__ dvals,
-    float* __restrict__ out, int64_t M, int64_t K, int64_t nnz, int64_t n_waves) {
+    const float* __restrict__ x, const float* __restrict__ xg, const float* __restrict__ dy,
+    float* __restrict__ dvals, float* __restrict__ out, int64_t M, int64_t K, int64_t nnz,
+    int64_t n_waves) {
   __shared__ int64_t bnd_s[kThreads / 64][kWin];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -458,12 +521,13 @@ __global__ __launch_bounds__(kThreads) void spmv_d1_bwd_kernel(
   if (s.pos >= s.b) return;
   if constexpr (VEC) {
     if (s.b <= (nnz & ~(int64_t)3)) {
-      bwd_walk<I, true, DV, MODE>(ptr, col, vals, x, dy, dvals, out, K, nnz, s, lane,
-                                  bnd_s[wave]);
+      bwd_walk<I, true, DV, MODE, GX>(ptr, col, vals, x, xg, dy, dvals, out, K, nnz, s, lane,
+                                      bnd_s[wave]);
       return;
     }
   }
-  bwd_walk<I, false, DV, MODE>(ptr, col, vals, x, dy, dvals, out, K, nnz, s, lane, bnd_s[wave]);
+  bwd_walk<I, false, DV, MODE, GX>(ptr, col, vals, x, xg, dy, dvals, out, K, nnz, s, lane,
+                                   bnd_s[wave]);
 }
 
 // -------------------------------------------- D == 1 dX: bucket sort + sum
@@ -1172,12 +1236,19 @@ int lanes_for(int64_t D, bool vec) {
   return units <= 4 ? 4 : (units <= 16 ? 16 : 64);
 }
 
+// Xg != nullptr (D == 1 only): also write Xg[p] = X[col[p]] for the
+// backward's dvals.
 template <typename I>
-int forward(const I* ptr, const I* col, const float* vals, const float* X, float* Y, int64_t M,
-            int64_t K, int64_t D, int64_t nnz, hipStream_t stream, const char* who) {
+int forward(const I* ptr, const I* col, const float* vals, const float* X, float* Y, float* Xg,
+            bool want_xg, int64_t M, int64_t K, int64_t D, int64_t nnz, hipStream_t stream,
+            const char* who) {
   const int64_t imax = sizeof(I) == 4 ? INT32_MAX : INT64_MAX / 2;
   int st = validate(M, K, D, nnz, imax, who);
   if (st) return st;
+  if (want_xg && D != 1)
+    return nl2k::fail(NL2K_ERR_SHAPE, "%s: the gathered copy of X needs D == 1 (got D=%lld)", who,
+                      (long long)D);
+  if (want_xg && nnz > 0 && !Xg) return nl2k::fail(NL2K_ERR_NULL, "%s: null pointer argument", who);
   if (M == 0) return nl2k::succeed();
   if (!ptr || !X || !Y || (nnz > 0 && (!col || !vals)))
     return nl2k::fail(NL2K_ERR_NULL, "%s: null pointer argument", who);
@@ -1185,13 +1256,17 @@ int forward(const I* ptr, const I* col, const float* vals, const float* X, float
     const int64_t n_waves = std::max<int64_t>(1, nl2k::ceil_div(nnz + M, kWaveItemsShort));
     const int64_t blocks = nl2k::ceil_div(n_waves, kThreads / 64);
     if (blocks > INT32_MAX) return nl2k::fail(NL2K_ERR_OVERFLOW, "%s: too many rows", who);
-    const bool vec = nl2k::aligned16(col) && nl2k::aligned16(vals);
-    if (vec)
-      hipLaunchKernelGGL((spmv_d1_fwd_kernel<I, true>), dim3((unsigned)blocks), dim3(kThreads), 0,
-                         stream, ptr, col, vals, X, Y, M, K, nnz, n_waves);
-    else
-      hipLaunchKernelGGL((spmv_d1_fwd_kernel<I, false>), dim3((unsigned)blocks), dim3(kThreads),
-                         0, stream, ptr, col, vals, X, Y, M, K, nnz, n_waves);
+    const bool save = want_xg && nnz > 0;
+    const bool vec = nl2k::aligned16(col) && nl2k::aligned16(vals) && (!save || nl2k::aligned16(Xg));
+#define D1_FWD(V, SV)                                                                       \
+  hipLaunchKernelGGL((spmv_d1_fwd_kernel<I, V, SV>), dim3((unsigned)blocks), dim3(kThreads), 0, \
+                     stream, ptr, col, vals, X, Y, Xg, M, K, nnz, n_waves)
+    if (vec) {
+      if (save) D1_FWD(true, true); else D1_FWD(true, false);
+    } else {
+      if (save) D1_FWD(false, true); else D1_FWD(false, false);
+    }
+#undef D1_FWD
     return nl2k::check_launch(who);
   }
   const bool vec = D % 4 == 0 && nl2k::aligned16(X) && nl2k::aligned16(Y);
@@ -1213,18 +1288,29 @@ int forward(const I* ptr, const I* col, const float* vals, const float* X, float
   return nl2k::check_launch(who);
 }
 
+// Xg != nullptr (dvals requested, mode kContrib or kNoDx): the gathered walk.
 template <typename I>
 void launch_d1_bwd(bool vec, bool dv, int mode, unsigned blocks, hipStream_t stream,
                    const I* ptr, const I* col, const float* vals, const float* X,
-                   const float* dY, float* dvals, float* out, int64_t M, int64_t K,
-                   int64_t nnz, int64_t n_waves) {
-#define D1_BWD(V, DVV, MM)                                                                   \
-  hipLaunchKernelGGL((spmv_d1_bwd_kernel<I, V, DVV, MM>), dim3(blocks), dim3(kThreads), 0, \
-                     stream, ptr, col, vals, X, dY, dvals, out, M, K, nnz, n_waves)
-#define D1_BWD_MODE(V, DVV)                     \
-  if (mode == kContrib) D1_BWD(V, DVV, kContrib); \
-  else if (mode == kAtomic) D1_BWD(V, DVV, kAtomic); \
-  else D1_BWD(V, DVV, kNoDx)
+                   const float* Xg, const float* dY, float* dvals, float* out, int64_t M,
+                   int64_t K, int64_t nnz, int64_t n_waves) {
+#define D1_BWD(V, DVV, MM, GG)                                                                   \
+  hipLaunchKernelGGL((spmv_d1_bwd_kernel<I, V, DVV, MM, GG>), dim3(blocks), dim3(kThreads), 0, \
+                     stream, ptr, col, vals, X, Xg, dY, dvals, out, M, K, nnz, n_waves)
+#define D1_BWD_MODE(V, DVV)                            \
+  if (mode == kContrib) D1_BWD(V, DVV, kContrib, false); \
+  else if (mode == kAtomic) D1_BWD(V, DVV, kAtomic, false); \
+  else D1_BWD(V, DVV, kNoDx, false)
+  if (dv && Xg != nullptr && mode != kAtomic) {
+    if (vec) {
+      if (mode == kContrib) D1_BWD(true, true, kContrib, true);
+      else D1_BWD(true, true, kNoDx, true);
+    } else {
+      if (mode == kContrib) D1_BWD(false, true, kContrib, true);
+      else D1_BWD(false, true, kNoDx, true);
+    }
+    return;
+  }
   if (vec) {
     if (dv) { D1_BWD_MODE(true, true); } else { D1_BWD_MODE(true, false); }
   } else {
@@ -1397,15 +1483,24 @@ int transpose_backward(const TransposePlan& tp, const I* ptr, const I* col, cons
   return nl2k::check_launch(who);
 }
 
+// Xg != nullptr (D == 1 only): dvals reads the forward's gathered copy of X
+// (spmv_forward_gather_*) instead of gathering, on the routes that do not
+// scatter by column (the bucket route and dvals alone).
 template <typename I>
-int backward(const I* ptr, const I* col, const float* vals, const float* X, const float* dY,
-             float* dvals, float* dX, int64_t M, int64_t K, int64_t D, int64_t nnz,
-             void* workspace, size_t ws_bytes, hipStream_t stream, const char* who) {
+int backward(const I* ptr, const I* col, const float* vals, const float* X, const float* Xg,
+             bool want_xg, const float* dY, float* dvals, float* dX, int64_t M, int64_t K,
+             int64_t D, int64_t nnz, void* workspace, size_t ws_bytes, hipStream_t stream,
+             const char* who) {
   const int64_t imax = sizeof(I) == 4 ? INT32_MAX : INT64_MAX / 2;
   int st = validate(M, K, D, nnz, imax, who);
   if (st) return st;
-  if (!ptr || !X || (M > 0 && !dY) || (nnz > 0 && (!col || !vals)))
+  if (want_xg && D != 1)
+    return nl2k::fail(NL2K_ERR_SHAPE, "%s: the gathered copy of X needs D == 1 (got D=%lld)", who,
+                      (long long)D);
+  if (!ptr || !X || (M > 0 && !dY) || (nnz > 0 && (!col || !vals)) ||
+      (want_xg && nnz > 0 && !Xg))
     return nl2k::fail(NL2K_ERR_NULL, "%s: null pointer argument", who);
+  if (!want_xg || nnz == 0) Xg = nullptr;
   const BucketPlan bp = bucket_plan(K, D, nnz);
   const bool sorted_dx = dX && bp.use && M > 0;
   if (sorted_dx) {
@@ -1426,9 +1521,10 @@ int backward(const I* ptr, const I* col, const float* vals, const float* X, cons
     uint16_t* low = reinterpret_cast<uint16_t*>(ws + bp.off_low);
     int64_t* meta = reinterpret_cast<int64_t*>(ws + bp.off_meta);
     const bool vec = nl2k::aligned16(col) && nl2k::aligned16(vals) &&
-                     (dvals == nullptr || nl2k::aligned16(dvals));
+                     (dvals == nullptr || nl2k::aligned16(dvals)) &&
+                     (Xg == nullptr || nl2k::aligned16(Xg));
     launch_d1_bwd<I>(vec, dvals != nullptr, kContrib, (unsigned)blocks, stream, ptr, col, vals,
-                     X, dY, dvals, contrib, M, K, nnz, n_waves);
+                     X, Xg, dY, dvals, contrib, M, K, nnz, n_waves);
     st = nl2k::check_launch(who);
     if (st) return st;
     if (nl2k::aligned16(col))
@@ -1468,9 +1564,10 @@ int backward(const I* ptr, const I* col, const float* vals, const float* X, cons
     const int64_t blocks = nl2k::ceil_div(n_waves, kThreads / 64);
     if (blocks > INT32_MAX) return nl2k::fail(NL2K_ERR_OVERFLOW, "%s: too many rows", who);
     const bool vec = nl2k::aligned16(col) && nl2k::aligned16(vals) &&
-                     (dvals == nullptr || nl2k::aligned16(dvals));
+                     (dvals == nullptr || nl2k::aligned16(dvals)) &&
+                     (Xg == nullptr || nl2k::aligned16(Xg));
     launch_d1_bwd<I>(vec, dvals != nullptr, dX ? kAtomic : kNoDx, (unsigned)blocks, stream, ptr,
-                     col, vals, X, dY, dvals, dX, M, K, nnz, n_waves);
+                     col, vals, X, Xg, dY, dvals, dX, M, K, nnz, n_waves);
     return nl2k::check_launch(who);
   }
   const bool vec = D % 4 == 0 && nl2k::aligned16(X) && nl2k::aligned16(dY) &&
@@ -1503,13 +1600,31 @@ const char* spmv_last_error(void) { return nl2k::error_slot().text; }
 int spmv_forward_f32_i32(const int32_t* row_ptr, const int32_t* col_idx, const float* vals,
                          const float* X, float* Y, int64_t M, int64_t K, int64_t D,
                          int64_t nnz, hipStream_t stream) {
-  return forward(row_ptr, col_idx, vals, X, Y, M, K, D, nnz, stream, "spmv_forward_f32_i32");
+  return forward(row_ptr, col_idx, vals, X, Y, (float*)nullptr, false, M, K, D, nnz, stream,
+                 "spmv_forward_f32_i32");
 }
 
 int spmv_forward_f32_i64(const int64_t* row_ptr, const int64_t* col_idx, const float* vals,
                          const float* X, float* Y, int64_t M, int64_t K, int64_t D,
                          int64_t nnz, hipStream_t stream) {
-  return forward(row_ptr, col_idx, vals, X, Y, M, K, D, nnz, stream, "spmv_forward_f32_i64");
+  return forward(row_ptr, col_idx, vals, X, Y, (float*)nullptr, false, M, K, D, nnz, stream,
+                 "spmv_forward_f32_i64");
+}
+
+int spmv_forward_gather_f32_i32(const int32_t* row_ptr, const int32_t* col_idx,
+                                const float* vals, const float* X, float* Y, float* Xg,
+                                int64_t M, int64_t K, int64_t D, int64_t nnz,
+                                hipStream_t stream) {
+  return forward(row_ptr, col_idx, vals, X, Y, Xg, true, M, K, D, nnz, stream,
+                 "spmv_forward_gather_f32_i32");
+}
+
+int spmv_forward_gather_f32_i64(const int64_t* row_ptr, const int64_t* col_idx,
+                                const float* vals, const float* X, float* Y, float* Xg,
+                                int64_t M, int64_t K, int64_t D, int64_t nnz,
+                                hipStream_t stream) {
+  return forward(row_ptr, col_idx, vals, X, Y, Xg, true, M, K, D, nnz, stream,
+                 "spmv_forward_gather_f32_i64");
 }
 
 size_t spmv_backward_workspace_bytes(int64_t M, int64_t K, int64_t D, int64_t nnz) {
@@ -1528,16 +1643,34 @@ int spmv_backward_f32_i32(const int32_t* row_ptr, const int32_t* col_idx, const 
                           const float* X, const float* dY, float* dvals, float* dX,
                           int64_t M, int64_t K, int64_t D, int64_t nnz, void* workspace,
                           size_t workspace_bytes, hipStream_t stream) {
-  return backward(row_ptr, col_idx, vals, X, dY, dvals, dX, M, K, D, nnz, workspace,
-                  workspace_bytes, stream, "spmv_backward_f32_i32");
+  return backward(row_ptr, col_idx, vals, X, (const float*)nullptr, false, dY, dvals, dX, M, K,
+                  D, nnz, workspace, workspace_bytes, stream, "spmv_backward_f32_i32");
 }
 
 int spmv_backward_f32_i64(const int64_t* row_ptr, const int64_t* col_idx, const float* vals,
                           const float* X, const float* dY, float* dvals, float* dX,
                           int64_t M, int64_t K, int64_t D, int64_t nnz, void* workspace,
                           size_t workspace_bytes, hipStream_t stream) {
-  return backward(row_ptr, col_idx, vals, X, dY, dvals, dX, M, K, D, nnz, workspace,
-                  workspace_bytes, stream, "spmv_backward_f32_i64");
+  return backward(row_ptr, col_idx, vals, X, (const float*)nullptr, false, dY, dvals, dX, M, K,
+                  D, nnz, workspace, workspace_bytes, stream, "spmv_backward_f32_i64");
+}
+
+int spmv_backward_gathered_f32_i32(const int32_t* row_ptr, const int32_t* col_idx,
+                                   const float* vals, const float* X, const float* Xg,
+                                   const float* dY, float* dvals, float* dX, int64_t M,
+                                   int64_t K, int64_t D, int64_t nnz, void* workspace,
+                                   size_t workspace_bytes, hipStream_t stream) {
+  return backward(row_ptr, col_idx, vals, X, Xg, true, dY, dvals, dX, M, K, D, nnz, workspace,
+                  workspace_bytes, stream, "spmv_backward_gathered_f32_i32");
+}
+
+int spmv_backward_gathered_f32_i64(const int64_t* row_ptr, const int64_t* col_idx,
+                                   const float* vals, const float* X, const float* Xg,
+                                   const float* dY, float* dvals, float* dX, int64_t M,
+                                   int64_t K, int64_t D, int64_t nnz, void* workspace,
+                                   size_t workspace_bytes, hipStream_t stream) {
+  return backward(row_ptr, col_idx, vals, X, Xg, true, dY, dvals, dX, M, K, D, nnz, workspace,
+                  workspace_bytes, stream, "spmv_backward_gathered_f32_i64");
 }
 
 }  // extern "C"

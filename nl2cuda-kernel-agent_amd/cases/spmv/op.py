@@ -1,7 +1,9 @@
 """CSR SpMM / SpMV candidate: autograd wrapper over libspmv_hip.so.
 
 Mirrors the reference's cases/spmv/op.py:24-57: ``_CSRSpMMFunction`` saves
-(row_ptr, col_idx, vals, X) and returns (None, None, grad_vals, grad_X);
+(row_ptr, col_idx, vals, X) (plus, at D == 1 when vals needs a gradient,
+the gathered X[col_idx] the forward read) and returns (None, None,
+grad_vals, grad_X);
 ``candidate`` / ``forward_only`` keep the dict interface.  The argument
 checks follow spmv.cu:167-197 (GPU tensors, fp32 values, 1-D structure of
 matching lengths, rank-2 X with positive sizes), with int32 indices accepted
@@ -30,8 +32,11 @@ def bind_library(lib):
     V, I64 = capi.c_void_p, capi.c_int64
     for t in ("i32", "i64"):
         capi.bind(lib, f"spmv_forward_f32_{t}", [V, V, V, V, V, I64, I64, I64, I64, V])
+        capi.bind(lib, f"spmv_forward_gather_f32_{t}", [V, V, V, V, V, V, I64, I64, I64, I64, V])
         capi.bind(lib, f"spmv_backward_f32_{t}",
                   [V, V, V, V, V, V, V, I64, I64, I64, I64, V, capi.c_size_t, V])
+        capi.bind(lib, f"spmv_backward_gathered_f32_{t}",
+                  [V, V, V, V, V, V, V, V, I64, I64, I64, I64, V, capi.c_size_t, V])
     capi.bind(lib, "spmv_backward_workspace_bytes", [I64, I64, I64, I64], restype=capi.c_size_t)
     capi.bind(lib, "spmv_status_offset", [I64, I64, I64, I64], restype=capi.c_size_t)
     capi.bind_last_error(lib, "spmv_last_error")
@@ -63,23 +68,42 @@ def _validate(row_ptr, col_idx, vals, X):
     return _suffix(row_ptr, col_idx)
 
 
-def spmv_forward(row_ptr, col_idx, vals, X):
+def spmv_forward(row_ptr, col_idx, vals, X, keep_gather=False):
+    """Y = A X.  keep_gather=True (D == 1 only) also returns Xg [nnz] =
+    X[col_idx] as the kernel read it, for spmv_backward(..., X_gathered=Xg)."""
     t = _validate(row_ptr, col_idx, vals, X)
     lib = _lib()
     row_ptr, col_idx, vals, X = (a.contiguous() for a in (row_ptr, col_idx, vals, X))
     M = row_ptr.numel() - 1
     K, D = X.shape
     Y = torch.empty((M, D), dtype=torch.float32, device=X.device)
+    if keep_gather:
+        capi.require(D == 1, "keep_gather needs D == 1")
+        Xg = torch.empty_like(vals)
     with torch.cuda.device(X.device):
-        st = getattr(lib, f"spmv_forward_f32_{t}")(
-            capi.ptr(row_ptr), capi.ptr(col_idx), capi.ptr(vals), capi.ptr(X), capi.ptr(Y),
-            M, K, D, vals.numel(), capi.stream_of(X))
+        if keep_gather:
+            st = getattr(lib, f"spmv_forward_gather_f32_{t}")(
+                capi.ptr(row_ptr), capi.ptr(col_idx), capi.ptr(vals), capi.ptr(X), capi.ptr(Y),
+                capi.ptr(Xg), M, K, D, vals.numel(), capi.stream_of(X))
+        else:
+            st = getattr(lib, f"spmv_forward_f32_{t}")(
+                capi.ptr(row_ptr), capi.ptr(col_idx), capi.ptr(vals), capi.ptr(X), capi.ptr(Y),
+                M, K, D, vals.numel(), capi.stream_of(X))
     capi.check(st, lib.spmv_last_error, "spmv_forward")
-    return Y
+    return (Y, Xg) if keep_gather else Y
 
 
-def spmv_backward(row_ptr, col_idx, vals, X, grad_Y, need_vals=True, need_X=True):
+def spmv_backward(row_ptr, col_idx, vals, X, grad_Y, need_vals=True, need_X=True,
+                  X_gathered=None):
+    """(grad_vals, grad_X).  X_gathered: the Xg spmv_forward(...,
+    keep_gather=True) returned for the same inputs; dvals then reads it
+    instead of gathering X (bit-identical results)."""
     t = _validate(row_ptr, col_idx, vals, X)
+    if X_gathered is not None:
+        capi.require(X.size(1) == 1, "X_gathered needs D == 1")
+        capi.require(X_gathered.is_cuda and X_gathered.dtype == torch.float32 and
+                     X_gathered.shape == vals.shape, "X_gathered must be a float32 GPU [nnz] tensor")
+        X_gathered = X_gathered.contiguous()
     capi.require(grad_Y.is_cuda and grad_Y.dtype == torch.float32, "grad_Y must be a float32 GPU tensor")
     M = row_ptr.numel() - 1
     capi.require(grad_Y.dim() == 2 and grad_Y.size(0) == M and grad_Y.size(1) == X.size(1),
@@ -97,11 +121,18 @@ def spmv_backward(row_ptr, col_idx, vals, X, grad_Y, need_vals=True, need_X=True
         if off != SIZE_MAX:
             status = ws[off:off + 8].view(torch.int64)
             status.zero_()
+    outs = (capi.ptr(grad_vals) if need_vals else None, capi.ptr(grad_X) if need_X else None)
     with torch.cuda.device(X.device):
-        st = getattr(lib, f"spmv_backward_f32_{t}")(
-            capi.ptr(row_ptr), capi.ptr(col_idx), capi.ptr(vals), capi.ptr(X), capi.ptr(grad_Y),
-            capi.ptr(grad_vals) if need_vals else None, capi.ptr(grad_X) if need_X else None,
-            M, K, D, vals.numel(), capi.ptr(ws), ws_bytes, capi.stream_of(X))
+        if X_gathered is not None:
+            st = getattr(lib, f"spmv_backward_gathered_f32_{t}")(
+                capi.ptr(row_ptr), capi.ptr(col_idx), capi.ptr(vals), capi.ptr(X),
+                capi.ptr(X_gathered), capi.ptr(grad_Y), *outs, M, K, D, vals.numel(),
+                capi.ptr(ws), ws_bytes, capi.stream_of(X))
+        else:
+            st = getattr(lib, f"spmv_backward_f32_{t}")(
+                capi.ptr(row_ptr), capi.ptr(col_idx), capi.ptr(vals), capi.ptr(X),
+                capi.ptr(grad_Y), *outs, M, K, D, vals.numel(), capi.ptr(ws), ws_bytes,
+                capi.stream_of(X))
     capi.check(st, lib.spmv_last_error, "spmv_backward")
     if status is not None:
         trips = int(status.item()) & 0xFFFFFFFF
@@ -110,21 +141,33 @@ def spmv_backward(row_ptr, col_idx, vals, X, grad_Y, need_vals=True, need_X=True
 
 
 class _CSRSpMMFunction(torch.autograd.Function):
+    """At D == 1 with vals requiring grad, the forward also keeps X[col_idx]
+    (nnz floats), so the backward's dvals streams it instead of gathering X
+    (the random reads that bound the D == 1 walk); gradients are
+    bit-identical either way."""
+
     @staticmethod
     def forward(ctx, row_ptr, col_idx, vals, X):
         row_ptr = row_ptr.contiguous()
         col_idx = col_idx.contiguous()
         vals = vals.contiguous()
         X = X.contiguous()
-        ctx.save_for_backward(row_ptr, col_idx, vals, X)
-        return spmv_forward(row_ptr, col_idx, vals, X)
+        keep = X.dim() == 2 and X.size(1) == 1 and ctx.needs_input_grad[2] and vals.numel() > 0
+        if keep:
+            Y, Xg = spmv_forward(row_ptr, col_idx, vals, X, keep_gather=True)
+            ctx.save_for_backward(row_ptr, col_idx, vals, X, Xg)
+        else:
+            Y = spmv_forward(row_ptr, col_idx, vals, X)
+            ctx.save_for_backward(row_ptr, col_idx, vals, X)
+        return Y
 
     @staticmethod
     def backward(ctx, grad_output):
-        row_ptr, col_idx, vals, X = ctx.saved_tensors
+        row_ptr, col_idx, vals, X, *kept = ctx.saved_tensors
         grad_vals, grad_X = spmv_backward(row_ptr, col_idx, vals, X, grad_output.contiguous(),
                                           need_vals=ctx.needs_input_grad[2],
-                                          need_X=ctx.needs_input_grad[3])
+                                          need_X=ctx.needs_input_grad[3],
+                                          X_gathered=kept[0] if kept else None)
         return None, None, grad_vals, grad_X
 
 

@@ -218,6 +218,34 @@ def test_spmv_argument_validation_without_gpu():
     assert st == STATUS["NL2K_ERR_ALIGN"]
 
 
+def test_spmv_gathered_entry_points_validate_without_gpu():
+    lib = _load("cases.spmv.op")
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: every call below fails validation
+    # the gathered copy of X exists only at D == 1
+    st = lib.spmv_forward_gather_f32_i32(fake, fake, fake, fake, fake, fake, 4, 4, 2, 8, None)
+    assert st == STATUS["NL2K_ERR_SHAPE"] and b"D == 1" in lib.spmv_last_error()
+    st = lib.spmv_backward_gathered_f32_i64(fake, fake, fake, fake, fake, fake, fake, fake, 4, 4,
+                                            3, 8, fake, 1 << 20, None)
+    assert st == STATUS["NL2K_ERR_SHAPE"] and b"D == 1" in lib.spmv_last_error()
+    # a null Xg is refused when there are nonzeros
+    st = lib.spmv_forward_gather_f32_i64(fake, fake, fake, fake, fake, None, 4, 4, 1, 8, None)
+    assert st == STATUS["NL2K_ERR_NULL"]
+    st = lib.spmv_backward_gathered_f32_i32(fake, fake, fake, fake, None, fake, fake, fake, 4, 4,
+                                            1, 8, fake, 1 << 20, None)
+    assert st == STATUS["NL2K_ERR_NULL"]
+    # shape checks come first, as in the plain entry points
+    st = lib.spmv_forward_gather_f32_i32(fake, fake, fake, fake, fake, fake, -1, 4, 1, 0, None)
+    assert st == STATUS["NL2K_ERR_SHAPE"] and b"M >= 0" in lib.spmv_last_error()
+    # same workspace contract as spmv_backward_f32_*
+    need = lib.spmv_backward_workspace_bytes(4, 4, 1, 8)
+    st = lib.spmv_backward_gathered_f32_i32(fake, fake, fake, fake, fake, fake, fake, fake, 4, 4,
+                                            1, 8, fake, need - 1, None)
+    assert st == STATUS["NL2K_ERR_WORKSPACE"]
+    # nothing to do: no rows
+    assert lib.spmv_forward_gather_f32_i32(fake, fake, fake, fake, fake, fake, 0, 4, 1, 0,
+                                           None) == 0
+
+
 def test_cosine_sim_argument_validation_without_gpu():
     lib = _load("cases.cosine_sim.op")
     fake = ctypes.c_void_p(1 << 20)  # never dereferenced: every call below fails validation

@@ -60,7 +60,26 @@ def _check(ptr, col, vals, X, seed=0, check_bwd=True):
         rdv, rdX = osp.backward_f64(ptr.numpy(), col.numpy(), vals.numpy(), X.numpy(), dY.numpy())
         _close("dvals", dv, rdv)
         _close("dX", dX, rdX)
+        if X.shape[1] == 1 and vals.numel() > 0:
+            _check_gathered(ptr, col, vals, X, dY, y, dv, rdX)
     return y
+
+
+def _check_gathered(ptr, col, vals, X, dY, y, dv, rdX):
+    """D == 1: the forward that keeps X[col] gives the same y bit for bit
+    and an exact copy of the gathered x; the backward reading that copy gives
+    the same dvals bit for bit (dX is summed in a varying order, so it is
+    checked against the oracle)."""
+    from cases.spmv import op
+    args = [ptr.cuda(), col.cuda(), vals.cuda(), X.cuda()]
+    y2, xg = op.spmv_forward(*args, keep_gather=True)
+    dv2, dX2 = op.spmv_backward(*args, dY.cuda(), X_gathered=xg)
+    dv3, _ = op.spmv_backward(*args, dY.cuda(), need_X=False, X_gathered=xg)
+    torch.cuda.synchronize()
+    assert torch.equal(y2, y), "gathered forward changed y"
+    assert torch.equal(xg.cpu(), X[:, 0][col.long()]), "Xg is not X[col]"
+    assert torch.equal(dv2, dv) and torch.equal(dv3, dv), "gathered dvals differ"
+    _close("dX (gathered walk)", dX2, rdX)
 
 
 @pytest.fixture(scope="module")
@@ -209,6 +228,48 @@ def test_spmv_misaligned_values():
     _close("y (misaligned X)", y, osp.forward_f64(ptr.numpy(), col.numpy(), vals.numpy(), X.numpy()))
 
 
+def test_spmv_autograd_keeps_gathered_x_at_d1():
+    """Through autograd at D == 1 with vals requiring grad the forward keeps
+    X[col] and the backward streams it: both gradients match the oracle and
+    the plain C-ABI backward."""
+    announce("spmv autograd D=1 with the gathered copy of X")
+    from cases.spmv import op
+    ptr, col, vals, X = _csr(np.minimum(np.random.default_rng(6).zipf(1.5, 5000), 3000), 3000, 1, 12)
+    vd = vals.cuda().requires_grad_(True)
+    Xd = X.cuda().requires_grad_(True)
+    y = op.candidate({"row_ptr": ptr.cuda(), "col_idx": col.cuda(), "vals": vd, "X": Xd}, {})
+    assert len(y.grad_fn.saved_tensors) == 5  # row_ptr, col_idx, vals, X, Xg
+    dY = torch.randn(y.shape, generator=torch.Generator().manual_seed(7))
+    y.backward(dY.cuda())
+    dv, _ = op.spmv_backward(ptr.cuda(), col.cuda(), vals.cuda(), X.cuda(), dY.cuda(), need_X=False)
+    torch.cuda.synchronize()
+    rdv, rdX = osp.backward_f64(ptr.numpy(), col.numpy(), vals.numpy(), X.numpy(), dY.numpy())
+    _close("dvals", vd.grad, rdv)
+    _close("dX", Xd.grad, rdX)
+    assert torch.equal(vd.grad, dv)
+
+
+def test_spmv_gathered_misaligned():
+    """Scalar (unaligned) forms of the gathered forward and walk."""
+    announce("spmv gathered copy of X, misaligned vals / Xg")
+    from cases.spmv import op
+    ptr, col, vals, X = _csr(np.random.default_rng(3).integers(0, 40, 1200), 900, 1, 13)
+    buf = torch.empty(vals.numel() + 1, device="cuda")
+    buf[1:].copy_(vals.cuda())
+    args = [ptr.cuda(), col.cuda(), buf[1:], X.cuda()]
+    y, xg = op.spmv_forward(*args, keep_gather=True)
+    xb = torch.empty(vals.numel() + 1, device="cuda")
+    xb[1:].copy_(xg)
+    dY = torch.randn(y.shape, generator=torch.Generator().manual_seed(8))
+    dv, dX = op.spmv_backward(*args, dY.cuda(), X_gathered=xb[1:])
+    torch.cuda.synchronize()
+    assert torch.equal(xg.cpu(), X[:, 0][col.long()])
+    rdv, rdX = osp.backward_f64(ptr.numpy(), col.numpy(), vals.numpy(), X.numpy(), dY.numpy())
+    _close("y", y, osp.forward_f64(ptr.numpy(), col.numpy(), vals.numpy(), X.numpy()))
+    _close("dvals", dv, rdv)
+    _close("dX", dX, rdX)
+
+
 def test_spmv_autograd_partial_grads():
     announce("spmv autograd, X only")
     from cases.spmv import op
@@ -232,3 +293,8 @@ def test_spmv_rejects_bad_arguments():
         op.spmv_forward(ptr.cuda(), col.cuda(), vals[:1].cuda(), X.cuda())
     with pytest.raises(RuntimeError, match="rank-2"):
         op.spmv_forward(ptr.cuda(), col.cuda(), vals.cuda(), X.reshape(-1).cuda())
+    with pytest.raises(RuntimeError, match="D == 1"):
+        op.spmv_forward(ptr.cuda(), col.cuda(), vals.cuda(), X.repeat(1, 2).cuda(), keep_gather=True)
+    with pytest.raises(RuntimeError, match="X_gathered must be"):
+        op.spmv_backward(ptr.cuda(), col.cuda(), vals.cuda(), X.cuda(), torch.ones(2, 1).cuda(),
+                         X_gathered=vals[:1].cuda())
