@@ -875,10 +875,12 @@ __global__ __launch_bounds__(kThreads) void spmm_bwd_kernel(
 //                            entries of one column land in position order
 //                            (within one 64-position step of a row, lanes
 //                            that share a column, found through LDS tags,
-//                            take slots in lane order).
+//                            take slots in lane order), as one 16-byte
+//                            record {row, position, value} per entry.
 //  S4 spmm_t_gather_kernel:  L lanes per column sum vals * dY[row] over the
-//                            column's entries in that order (and, when asked
-//                            and D fits one pass, dvals[p] = dY[row] . X[c]).
+//                            column's entries in that order, 16 entries per
+//                            step (and, when asked and D fits one pass,
+//                            dvals[p] = dY[row] . X[c]).
 constexpr int kTransposeMaxCols = 16384;  // LDS of the chunk kernels (5 B per column)
 constexpr int64_t kTransposeChunk = 1024;  // positions per chunk, at least
 
@@ -1060,8 +1062,8 @@ constexpr int kScatterRowWin = 2048;  // row starts of a chunk staged in LDS
 template <typename I>
 __global__ __launch_bounds__(kThreads) void spmm_t_scatter_kernel(
     const I* __restrict__ ptr, const I* __restrict__ col, const float* __restrict__ vals,
-    const int* __restrict__ O, I* __restrict__ crow, I* __restrict__ cpos,
-    float* __restrict__ cval, int64_t M, int64_t K, int64_t nnz, int64_t P) {
+    const int* __restrict__ O, i32x4_t* __restrict__ crec, int64_t M, int64_t K, int64_t nnz,
+    int64_t P) {
   extern __shared__ int lds_i[];  // K cursors, then K tag bytes
   unsigned char* tag = reinterpret_cast<unsigned char*>(lds_i + K);
   __shared__ long long s_rows[2];
@@ -1145,9 +1147,7 @@ __global__ __launch_bounds__(kThreads) void spmm_t_scatter_kernel(
           if (act) {
             atomicAdd(&lds_i[cc[k]], 1);
             const int64_t pos = max((int64_t)0, min((int64_t)base + rank, nnz - 1));
-            crow[pos] = (I)rr[k];
-            cpos[pos] = (I)q;
-            cval[pos] = vv[k];
+            crec[pos] = i32x4_t{(int)rr[k], (int)q, __float_as_int(vv[k]), 0};
           }
         }
         // the next wave reads the cursors this one advanced: LDS order only
@@ -1161,17 +1161,33 @@ __global__ __launch_bounds__(kThreads) void spmm_t_scatter_kernel(
   }
 }
 
+// Column c's entries, 16 per step: the group's lanes load the step's
+// records (lane gl records gl, gl + L, ...; 16-byte {row, position, value})
+// and shuffle each entry's fields to the whole group, which then loads the
+// 16 dY rows together; the next step's records are loaded while those rows
+// are in flight.  Entries past the column's end repeat its last entry (valid
+// addresses) and are masked out of the sums and stores.
 template <typename I, int L, bool VEC, bool DV>
 __global__ __launch_bounds__(kThreads) void spmm_t_gather_kernel(
-    const I* __restrict__ colptr, const I* __restrict__ crow, const I* __restrict__ cpos,
-    const float* __restrict__ cval, const float* __restrict__ X, const float* __restrict__ dY,
-    float* __restrict__ dX, float* __restrict__ dvals, int64_t M, int64_t K, int64_t D,
-    int64_t nnz) {
+    const I* __restrict__ colptr, const i32x4_t* __restrict__ crec,
+    const float* __restrict__ X, const float* __restrict__ dY, float* __restrict__ dX,
+    float* __restrict__ dvals, int64_t M, int64_t K, int64_t D, int64_t nnz) {
   using V = Lanes<VEC>;
+  constexpr int E = 16;                   // entries per step
+  constexpr int RPL = (E + L - 1) / L;    // records per lane per step
   const int64_t c = (int64_t)blockIdx.x * (kThreads / L) + threadIdx.x / L;
   const int gl = threadIdx.x % L;
+  const int gbase = (threadIdx.x & 63) - gl;  // first lane of the group in the wave
   if (c >= K) return;  // whole groups exit together (L divides 64)
   const int64_t s = ld_ptr(colptr, c, nnz), e = max(s, ld_ptr(colptr, c + 1, nnz));
+  if (s == e) {
+    for (int64_t d = (int64_t)gl * V::W; d < D; d += (int64_t)L * V::W) V::store(dX + c * D + d, V::zero());
+    return;
+  }
+  auto load_recs = [&](int64_t q, i32x4_t (&r)[RPL]) {
+#pragma unroll
+    for (int j = 0; j < RPL; ++j) r[j] = crec[max(s, min(q + gl + (int64_t)L * j, e - 1))];
+  };
   for (int64_t d0 = 0; d0 < D; d0 += (int64_t)L * V::W) {
     const int64_t d = d0 + (int64_t)gl * V::W;
     const bool active = d < D;
@@ -1179,31 +1195,63 @@ __global__ __launch_bounds__(kThreads) void spmm_t_gather_kernel(
     typename V::T xc = V::zero();
     if (DV) xc = V::load(X + c * D + dc);
     typename V::T acc = V::zero();
-    // four entries per step; the last step's missing entries repeat entry
-    // e - 1 (valid addresses) and are masked out of the sums and stores
-    for (int64_t q = s; q < e; q += 4) {
-      int64_t rr[4], pp[4];
-      float vv[4];
+    i32x4_t rec[RPL];
+    load_recs(s, rec);
+    for (int64_t q = s; q < e; q += E) {
+      const int my_pos = rec[0][1];  // L == 16: lane gl holds entry gl's record
+      int rr[E], pp[E];
+      float vv[E];  // zero past the column's end, so the sum needs no branch
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int64_t qu = min(q + u, e - 1);
-        rr[u] = min(max((int64_t)crow[qu], (int64_t)0), M - 1);
-        vv[u] = cval[qu];
-        if (DV) pp[u] = min(max((int64_t)cpos[qu], (int64_t)0), nnz - 1);
+      for (int u = 0; u < E; ++u) {
+        const int src = gbase + (u % L);
+        rr[u] = __shfl(rec[u / L][0], src, 64);
+        const float v = __int_as_float(__shfl(rec[u / L][2], src, 64));
+        vv[u] = q + u < e ? v : 0.f;
+        if (DV) pp[u] = __shfl(rec[u / L][1], src, 64);
       }
-      typename V::T gs[4];
+      typename V::T gs[E];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) gs[u] = V::load(dY + rr[u] * D + dc);
+      for (int u = 0; u < E; ++u) {
+        const int64_t r = min(max((int64_t)rr[u], (int64_t)0), M - 1);
+        gs[u] = V::load(dY + r * D + dc);
+      }
+      load_recs(q + E, rec);
+      // every row load is in flight before the first use (left alone, the
+      // compiler sinks each load to its add and waits for it there)
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (q + u < e) acc += vv[u] * gs[u];
-      if (DV) {
+      for (int u = 0; u < E; ++u) acc += vv[u] * gs[u];
+      if constexpr (DV && L == 16) {
+        // Reduce-scatter of the 16 partial dots over the group's 16 lanes
+        // (halving butterfly): afterwards lane gl holds entry gl's dot,
+        // 15 exchanges for the step instead of a 4-level reduction per entry.
+        float v[E];
+#pragma unroll
+        for (int u = 0; u < E; ++u) v[u] = active ? V::dot(gs[u], xc) : 0.f;
+        auto level = [&](auto hc) {
+          constexpr int h = decltype(hc)::value;
+          const bool upper = (gl & h) != 0;
+#pragma unroll
+          for (int k = 0; k < h; ++k) {
+            const float keep = upper ? v[k + h] : v[k];
+            const float send = upper ? v[k] : v[k + h];
+            v[k] = keep + __shfl_xor(send, h, 16);
+          }
+        };
+        level(std::integral_constant<int, 8>{});
+        level(std::integral_constant<int, 4>{});
+        level(std::integral_constant<int, 2>{});
+        level(std::integral_constant<int, 1>{});
+        const int64_t pu = min(max((int64_t)my_pos, (int64_t)0), nnz - 1);
+        if (q + gl < e) dvals[pu] = v[0];
+      } else if constexpr (DV) {
         // every lane of the group stores the (identical) group sum: a
-        // one-lane branch would hold the position loads inside it
+        // one-lane branch would hold the stores' addresses inside it
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < E; ++u) {
           const float dt = group_sum<L>(active ? V::dot(gs[u], xc) : 0.f);
-          if (q + u < e) dvals[pp[u]] = dt;
+          const int64_t pu = min(max((int64_t)pp[u], (int64_t)0), nnz - 1);
+          if (q + u < e) dvals[pu] = dt;
         }
       }
     }
@@ -1353,13 +1401,13 @@ BucketPlan bucket_plan(int64_t K, int64_t D, int64_t nnz) {
 // Stable transpose for dX at D > 1 (spmm_t_* kernels); workspace sections
 // 256-byte aligned: trip counter (8 B, first, so its offset does not depend
 // on the index type), look-back slots [n_blocks] (16 B), H [n_chunks][K]
-// (int32 counts, then first slots), colptr [K+1] (I), crow / cpos [nnz]
-// (I), cval [nnz].  Chunks of P positions, about one per CU.
+// (int32 counts, then first slots), colptr [K+1] (I), records [nnz] (16 B:
+// int32 row, int32 position, fp32 value, pad; nnz < 2^31 and M < 2^31).
+// Chunks of P positions, about one per CU.
 struct TransposePlan {
   bool use = false;
   int64_t P = 0, n_chunks = 0, n_blocks = 0;
-  size_t off_status = 0, off_slots = 0, off_H = 0, off_colptr = 0, off_crow = 0, off_cpos = 0,
-         off_cval = 0, bytes = 0;
+  size_t off_status = 0, off_slots = 0, off_H = 0, off_colptr = 0, off_rec = 0, bytes = 0;
 };
 
 TransposePlan transpose_plan(int64_t M, int64_t K, int64_t D, int64_t nnz, size_t isz) {
@@ -1382,12 +1430,8 @@ TransposePlan transpose_plan(int64_t M, int64_t K, int64_t D, int64_t nnz, size_
   off += align256((size_t)(p.n_chunks * K) * sizeof(int));
   p.off_colptr = off;
   off += align256((size_t)(K + 1) * isz);
-  p.off_crow = off;
-  off += align256((size_t)nnz * isz);
-  p.off_cpos = off;
-  off += align256((size_t)nnz * isz);
-  p.off_cval = off;
-  p.bytes = off + align256((size_t)nnz * sizeof(float));
+  p.off_rec = off;
+  p.bytes = off + align256((size_t)nnz * 16);
   return p;
 }
 
@@ -1407,9 +1451,7 @@ int transpose_backward(const TransposePlan& tp, const I* ptr, const I* col, cons
   I* colptr = reinterpret_cast<I*>(ws + tp.off_colptr);
   unsigned long long* slots = reinterpret_cast<unsigned long long*>(ws + tp.off_slots);
   unsigned* trips = reinterpret_cast<unsigned*>(ws + tp.off_status);
-  I* crow = reinterpret_cast<I*>(ws + tp.off_crow);
-  I* cpos = reinterpret_cast<I*>(ws + tp.off_cpos);
-  float* cval = reinterpret_cast<float*>(ws + tp.off_cval);
+  i32x4_t* crec = reinterpret_cast<i32x4_t*>(ws + tp.off_rec);
   hipError_t qe = hipSuccess;
   const bool cap = nl2k::slots::capturing(stream, &qe);
   if (qe != hipSuccess) return nl2k::check_hip(qe, "hipStreamIsCapturing");
@@ -1438,7 +1480,7 @@ int transpose_backward(const TransposePlan& tp, const I* ptr, const I* col, cons
   st = nl2k::check_launch(who);
   if (st) return st;
   hipLaunchKernelGGL((spmm_t_scatter_kernel<I>), dim3((unsigned)tp.n_chunks), dim3(kThreads), lds_s,
-                     stream, ptr, col, vals, H, crow, cpos, cval, M, K, nnz, tp.P);
+                     stream, ptr, col, vals, H, crec, M, K, nnz, tp.P);
   st = nl2k::check_launch(who);
   if (st) return st;
   const bool vec = D % 4 == 0 && nl2k::aligned16(X) && nl2k::aligned16(dY) &&
@@ -1449,7 +1491,7 @@ int transpose_backward(const TransposePlan& tp, const I* ptr, const I* col, cons
   const dim3 grid((unsigned)blocks), block(kThreads);
 #define SPMM_T(LL, VV, DVV)                                                                   \
   hipLaunchKernelGGL((spmm_t_gather_kernel<I, LL, VV, DVV>), grid, block, 0, stream, colptr, \
-                     crow, cpos, cval, X, dY, dX, dvals, M, K, D, nnz)
+                     crec, X, dY, dX, dvals, M, K, D, nnz)
 #define SPMM_T_L(VV, DVV)                     \
   if (L == 4) SPMM_T(4, VV, DVV);             \
   else if (L == 16) SPMM_T(16, VV, DVV);      \

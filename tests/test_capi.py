@@ -194,14 +194,14 @@ def test_spmv_argument_validation_without_gpu():
     assert lib.spmv_backward_workspace_bytes(100, 7, 1, 10) == 256 + 256 + 1 * 2 * 8  # 1 bucket
     assert lib.spmv_backward_workspace_bytes(K, K, 64, nnz) == 0  # D > 1, K > 16384: atomics
     # D > 1 with K <= 16384: the column-major copy of A (trip counter and look-back
-    # slots first, then chunk offsets, colptr, rows, positions, values)
+    # slots first, then chunk offsets, colptr, 16-byte {row, position, value} records)
     n2 = 64 * 4096
     ws2 = lib.spmv_backward_workspace_bytes(4096, 4096, 64, n2)
     def a256(b):
         return (b + 255) // 256 * 256
     chunks = n2 // 1024  # 1024 positions per chunk, int32 chunk counts; 8-byte indices
     assert ws2 == 256 + a256(256 * 16) + a256(chunks * 4096 * 4) + a256(4097 * 8) \
-        + 2 * a256(n2 * 8) + a256(n2 * 4)
+        + a256(n2 * 16)
     assert lib.spmv_status_offset(4096, 4096, 64, n2) == 0
     SIZE_MAX = ctypes.c_size_t(-1).value
     assert lib.spmv_status_offset(K, K, 1, nnz) == SIZE_MAX  # D == 1: bucket route
