@@ -989,31 +989,40 @@ __global__ __launch_bounds__(kThreads) void spmm_t_offsets_kernel(
     if (lane < kOffCols) s_cpre[lane] = incl - ct;
     const long long block_total = __shfl(incl, 63, 64);
     if (lane == 0) nl2k::slots::publish(slots, blockIdx.x, (unsigned long long)block_total, key);
-    long long prev = 0;
-    for (int base = 0; base < (int)blockIdx.x; base += 64) {
-      const int bb = base + lane;
-      long long v = 0;
-      if (bb < (int)blockIdx.x) {
-        unsigned long long x0 = nl2k::slots::load_word(slots + 2 * bb);
-        unsigned long long x1 = nl2k::slots::load_word(slots + 2 * bb + 1);
-        unsigned spins = 0;
-        while (!nl2k::slots::ready(x0, x1, key)) {
-          if (++spins > (1u << 24)) {  // never expected: report and give up
-            __hip_atomic_fetch_add(trips, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            x0 = key.m0;
-            break;
-          }
-          __builtin_amdgcn_s_sleep(1);
-          x0 = nl2k::slots::load_word(slots + 2 * bb);
-          x1 = nl2k::slots::load_word(slots + 2 * bb + 1);
-        }
-        v = (long long)nl2k::slots::decode(x0, key);
+    // The earlier blocks' totals, 256 slots per round: every slot of a round
+    // is loaded before any is waited on, so a round costs one round trip.
+    const int nprev = (int)blockIdx.x;
+    long long v = 0;
+    for (int base = 0; base < nprev; base += 4 * 64) {
+      unsigned long long x0[4], x1[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int bb = min(base + 64 * k + lane, nprev - 1);
+        x0[k] = nl2k::slots::load_word(slots + 2 * bb);
+        x1[k] = nl2k::slots::load_word(slots + 2 * bb + 1);
       }
 #pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-      prev += v;
+      for (int k = 0; k < 4; ++k) {
+        const int bb = base + 64 * k + lane;
+        if (bb < nprev) {
+          unsigned spins = 0;
+          while (!nl2k::slots::ready(x0[k], x1[k], key)) {
+            if (++spins > (1u << 24)) {  // never expected: report and give up
+              __hip_atomic_fetch_add(trips, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              x0[k] = key.m0;
+              break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            x0[k] = nl2k::slots::load_word(slots + 2 * bb);
+            x1[k] = nl2k::slots::load_word(slots + 2 * bb + 1);
+          }
+          v += (long long)nl2k::slots::decode(x0[k], key);
+        }
+      }
     }
-    if (lane == 0) s_prev = prev;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    if (lane == 0) s_prev = v;
   }
   __syncthreads();
   if (c < K) {
