@@ -219,6 +219,19 @@ def spmv(dev, time_us):
                                 lib, "spmv_last_error"))
     out.append(("spmv", "backward dvals + dx, zipf 2^20", tt, base + 4 * M + 8 * K + 4 * nnz,
                 "read structure, dy, x; write dvals, dx"))
+    # the autograd pair when vals needs a gradient: the forward keeps x[col]
+    # and the backward streams it
+    xg = torch.empty_like(vals)
+    tt = time_us(lambda: _check(lib.spmv_forward_gather_f32_i32(P(ptr), P(col), P(vals), P(X), P(Y),
+                                                               P(xg), M, K, 1, nnz, s),
+                                lib, "spmv_last_error"))
+    out.append(("spmv", "forward keeping x[col], zipf 2^20", tt, base + 4 * K + 4 * M + 4 * nnz,
+                "read row_ptr, col_idx, vals, x; write y, x[col]"))
+    tt = time_us(lambda: _check(lib.spmv_backward_gathered_f32_i32(
+        P(ptr), P(col), P(vals), P(X), P(xg), P(dY), P(dv), P(dX), M, K, 1, nnz, P(ws), wsb, s),
+        lib, "spmv_last_error"))
+    out.append(("spmv", "backward dvals + dx from kept x[col], zipf 2^20", tt,
+                base + 4 * M + 4 * K + 8 * nnz, "read structure, dy, x[col]; write dvals, dx"))
     return out
 
 
