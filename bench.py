@@ -28,11 +28,14 @@ seed checked), LayerNorm [8192, 4096] (fwd, bwd), scan [64, 65536] (fp32
 fwd, bwd; int32 -> int64 fwd, bit-exact), CSR SpMV on the Zipf 2^20 matrix
 (fwd; bwd dX; bwd dvals + dX; and the autograd pair when vals needs a
 gradient: fwd keeping X[col], bwd dvals + dX from it), and the reference's
-default SpMM (M = K =
-4096, D = 64; fwd; bwd dvals + dX).  Each entry gives event us, GB/s, the
-fraction of its binding roof (fp32 MFMA for RBF, HBM otherwise), and
-max_abs / max_rel per output against the float64 oracle, plus the time of
-the reference's PyTorch CPU path for that call on this host.
+default SpMM (M = K = 4096, D = 64; fwd; bwd dvals + dX).  Each entry gives
+event us, GB/s, the fraction of its binding roof (fp32 MFMA for RBF, HBM
+otherwise), and max_abs / max_rel per output against the float64 oracle,
+plus the time of the reference's PyTorch CPU path for that call on this
+host.  Entries with a committed rocprofv3 traffic summary (profiles/
+*_traffic.json: FETCH_SIZE and WRITE_SIZE scaled by a plain copy's
+readings) also carry ``traffic``: measured HBM bytes per launch, their
+ratio to the algorithmic bytes, and the source file.
 
 CPU leg (the only code here that imports oracle/): ``cpu_baseline`` times the
 reference's PyTorch CPU path (cases/rbf/reference.py:14-20 forward, autograd
@@ -188,6 +191,40 @@ class RbfGpu:
                 "dY": self.dY.cpu().numpy()}
 
 
+# Per-config HBM traffic from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+# summaries (profile.py traffic, scaled by a plain copy's readings), keyed by
+# (config label prefix, call).
+TRAFFIC_PROFILES = {
+    ("rbf N=M=4096", "forward"): "rbf_fwd_4096",
+    ("rbf N=M=4096", "backward"): "rbf_bwd_4096",
+    ("layernorm", "forward"): "layernorm_fwd_8192x4096",
+    ("layernorm", "backward"): "layernorm_bwd_8192x4096",
+    ("scan", "forward_f32"): "scan_fwd_f32_64x65536",
+    ("scan", "backward_f32"): "scan_bwd_f32_64x65536",
+    ("scan", "forward_i32_i64"): "scan_fwd_i32_i64_64x65536",
+    ("spmv zipf", "forward"): "spmv_fwd_zipf_2p20",
+    ("spmv zipf", "backward dX"): "spmv_bwd_dx_zipf_2p20",
+}
+
+
+def profiled_traffic(config, call, nbytes):
+    """{hbm_bytes, over_algorithmic, source} for a config entry that has a
+    committed traffic profile, else None."""
+    for (prefix, c), name in TRAFFIC_PROFILES.items():
+        if config.startswith(prefix) and call == c:
+            path = os.path.join("profiles", f"{name}_traffic.json")
+            try:
+                with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), path)) as f:
+                    hbm = json.load(f).get("hbm_bytes_per_launch")
+            except (OSError, ValueError):
+                return None
+            if not hbm:
+                return None
+            return {"hbm_bytes": int(hbm), "over_algorithmic": round(hbm / nbytes, 3),
+                    "source": path}
+    return None
+
+
 def _entry(config, call, us_samples, nbytes, flops=None, bound="hbm", extra=None):
     us, cv = repeat_stats(us_samples)
     gbs = nbytes / (us * 1e-6) / 1e9
@@ -200,6 +237,9 @@ def _entry(config, call, us_samples, nbytes, flops=None, bound="hbm", extra=None
                  pct_fp32=round(100 * tf / FP32_PEAK_TFLOPS, 2))
     frac = (e["tflops"] / FP32_PEAK_TFLOPS) if bound == "mfma" else gbs / HBM_PEAK_GBS
     e["roofline"] = {"bound": bound, "frac": round(frac, 4)}
+    traffic = profiled_traffic(config, call, nbytes)
+    if traffic:
+        e["traffic"] = traffic
     if extra:
         e.update(extra)
     return e
