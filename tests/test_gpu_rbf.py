@@ -96,7 +96,10 @@ def test_rbf_8192_parity_and_identities(seed):
 
 
 @pytest.mark.parametrize("n,m", [(1, 1), (3, 5), (65, 130), (127, 129), (300, 17),
-                                 (128, 4100), (1000, 999), (513, 2049)])
+                                 (128, 4100), (1000, 999), (513, 2049),
+                                 # multiples of 64: the full-tile (buffer-load) backward
+                                 # at every region width, square and not
+                                 (64, 192), (256, 640), (1088, 960), (3072, 1024)])
 def test_rbf_ragged_shapes(n, m):
     announce(f"rbf ragged n={n} m={m}")
     _check_full(*_inputs(n, m, 64, n + m), 0.5)
