@@ -65,8 +65,9 @@ constexpr int kStep = 64 * kPer;        // positions per wave step
 constexpr int kWin = 512;               // row starts staged per LDS window (per wave)
 // Rows + nonzeros per wave (D == 1).  Halving the forward's range (more
 // waves, more gathers in flight per CU) took the forward from 150 to 142 us
-// and the dvals + dX backward from 269 to 260 us; the dX-only backward is
-// best with the longer range (143 against 147 us).
+// and the dvals + dX backward from 269 to 260 us; the walks that gather
+// nothing (dX only, and dvals from the forward's gathered copy) are best
+// with the longer range (143 against 147 us; 65 against 72 us).
 constexpr int64_t kWaveItemsShort = 2048;
 constexpr int64_t kWaveItemsLong = 4096;
 
@@ -1561,7 +1562,10 @@ int backward(const I* ptr, const I* col, const float* vals, const float* X, cons
     if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
       return nl2k::fail(NL2K_ERR_ALIGN, "%s: workspace must be 256-byte aligned", who);
   }
-  const int64_t wave_items = dvals ? kWaveItemsShort : kWaveItemsLong;
+  // the walk gathers x for dvals unless it reads the gathered copy (the
+  // atomic dX route, beyond the bucket limits, always gathers)
+  const bool gathers = dvals && !(Xg && (sorted_dx || !dX));
+  const int64_t wave_items = gathers ? kWaveItemsShort : kWaveItemsLong;
   if (sorted_dx) {
     const int64_t n_waves = std::max<int64_t>(1, nl2k::ceil_div(nnz + M, wave_items));
     const int64_t blocks = nl2k::ceil_div(n_waves, kThreads / 64);
