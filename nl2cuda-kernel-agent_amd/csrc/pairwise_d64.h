@@ -565,7 +565,7 @@ __global__ __launch_bounds__(512) void pair_bwd_d64_kernel(
 // every accumulator sees the same MFMA sequence, so the partials are
 // bit-identical to pair_bwd_d64_kernel's.  The role index is read through
 // readfirstlane so the compiler sees wave-uniform branches and gives each
-// role its own live ranges (168 VGPRs, three waves per SIMD).
+// role its own live ranges (at most 168 VGPRs: three waves per SIMD).
 // kFull (N and M multiples of 64, every byte offset of dK / K below 2^31):
 // no tile is ragged, so the staging waves load through buffer resources
 // with the tile's offset in a scalar register and a fixed per-lane offset,
