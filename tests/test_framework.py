@@ -94,3 +94,29 @@ def test_loader_refuses_a_stale_library(tmp_path, monkeypatch):
     monkeypatch.setenv("NL2K_ALLOW_STALE", "1")
     with pytest.raises(OSError):  # gets as far as dlopen of the (fake) file
         loader.load_library("k", ["k.hip"], str(tmp_path))
+
+
+def test_loader_builds_and_loads_a_tiny_library(tmp_path, monkeypatch):
+    """hipcc cross-compiles for gfx950 without a GPU; the host side of the
+    library is callable here, and the build stamp makes it fresh."""
+    from framework import loader
+    src = tmp_path / "t.hip"
+    src.write_text('extern "C" int nl2k_answer(int x) { return 2 * x + 1; }\n')
+    path = loader.build_library("t", ["t.hip"], str(tmp_path))
+    assert path.endswith("libt.so") and not loader.is_stale("t", ["t.hip"], str(tmp_path))
+    monkeypatch.delenv("NL2K_ALLOW_STALE", raising=False)
+    lib = loader.load_library("t", ["t.hip"], str(tmp_path))
+    assert lib.nl2k_answer(20) == 41
+
+
+def test_loader_reports_build_failures(tmp_path):
+    """A source that does not compile, or a missing one, raises with the
+    compiler's message instead of leaving a library behind."""
+    import pytest
+    from framework import loader
+    (tmp_path / "bad.hip").write_text('extern "C" int f(void) { return undefined_name; }\n')
+    with pytest.raises(RuntimeError, match="hipcc failed for libbad.so"):
+        loader.build_library("bad", ["bad.hip"], str(tmp_path))
+    assert not (tmp_path / "libbad.so").exists()
+    with pytest.raises(FileNotFoundError, match="source file not found"):
+        loader.build_library("gone", ["gone.hip"], str(tmp_path))
