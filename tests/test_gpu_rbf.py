@@ -207,10 +207,14 @@ def test_rbf_repeatable():
         assert torch.equal(x, y)
 
 
-def test_rbf_verify_all_framework():
-    """The framework's parity harness (reference verify.py protocol) at 2048."""
-    announce("rbf verify_all 2048 (CPU torch reference path)")
+@pytest.mark.parametrize("size", [2048, 4096])
+def test_rbf_verify_all_framework(size):
+    """The framework's parity harness (the reference's verify.py protocol:
+    five seeds, the case's own reference.py through autograd, here run by
+    torch on the device, 4 GiB of broadcast intermediate at 4096) at config
+    sizes 1 and 2."""
+    announce(f"rbf verify_all {size} (case reference.py path)")
     from cases.rbf import baseline_case, op
-    ok, report = verify_all(baseline_case(2048), op.candidate, device="cuda")
+    ok, report = verify_all(baseline_case(size), op.candidate, device="cuda")
     print(report)
     assert ok, report
