@@ -732,7 +732,7 @@ def copy_calibration():
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=60)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--size", type=int, default=4096)
     ap.add_argument("--cpu-budget", type=float, default=15.0,
@@ -741,7 +741,7 @@ def main():
     ap.add_argument("--configs", default="all",
                     help="comma list of rbf2048,rbf4096,rbf8192,layernorm,scan,spmv,spmm, "
                          "'all' or 'none' (headline only)")
-    ap.add_argument("--config-iters", type=int, default=30,
+    ap.add_argument("--config-iters", type=int, default=100,
                     help="timed calls per config entry (three repeats)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device-to-device copy 10 times (the known-size "
