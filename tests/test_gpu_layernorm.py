@@ -56,7 +56,7 @@ def _check(x, w, bias, dy, xdev=None):
     _close("dbeta", db, rdb)
 
 
-@pytest.mark.parametrize("seed", [0, 1])
+@pytest.mark.parametrize("seed", [0, 1, 2, 3, 4])
 def test_layernorm_baseline_8192x4096(seed):
     announce(f"layernorm 8192x4096 seed={seed}")
     _check(*_inputs(8192, 4096, seed))

@@ -56,7 +56,7 @@ def _op():
     return op
 
 
-@pytest.mark.parametrize("seed", [0, 1, 2])
+@pytest.mark.parametrize("seed", [0, 1, 2, 3, 4])
 def test_scan_f32_baseline_64x65536(seed):
     announce(f"scan f32 [64, 65536] seed={seed}")
     op = _op()
@@ -70,7 +70,7 @@ def test_scan_f32_baseline_64x65536(seed):
     _close("dx", xd.grad, osc.reverse_cumsum_f32(dy.numpy()), min_equal=0.999)
 
 
-@pytest.mark.parametrize("seed", [0, 1])
+@pytest.mark.parametrize("seed", [0, 1, 2, 3, 4])
 def test_scan_i32_to_i64_bit_exact(seed):
     announce(f"scan int32 -> int64 [64, 65536] seed={seed}")
     x = _ints(64, 65536, seed)
