@@ -21,20 +21,22 @@
 //    lanes' trailing partial sums, and every row that ends inside the step
 //    is written once; the row still open at the end of the step is carried
 //    in registers.  Empty rows are written as 0 by whoever sees the gap.
-//  * D == 1 backward: the same walk gives each position its row; the wave
-//    writes dvals and the contribution vals[p] * dy[row(p)] of every
-//    position with 16-byte stores, in position order.  dX = A^T dy is then
-//    a sum by column without atomics (random 4-byte atomics or stores run at
-//    the L2's request rate, ~20 G/s and ~170 G/s here, far below streaming):
-//    a sort kernel reads tiles of 16384 positions (contribution and column),
-//    counts them per column bucket (2^k columns, about 256 buckets) in LDS,
-//    orders the tile by bucket in LDS and writes it back in place with the
-//    low column bits beside it, plus each bucket's segment offsets; one
-//    workgroup per bucket then sums its segments of every tile into an LDS
-//    copy of its dX slice (compare-and-swap float adds) and writes the slice
-//    once.  The order of the additions within a column varies between runs,
-//    as with the reference's atomics.  Column counts too large for 1024 buckets of
-//    16384 columns fall back to zero-fill plus fp32 atomics.
+//  * D == 1 backward, dvals alone: the same walk gives each position its
+//    row; the wave writes dvals with 16-byte stores, in position order.
+//  * D == 1 backward with dX: dX = A^T dy is a sum by column, done without
+//    atomics (random 4-byte atomics or stores run at the L2's request rate,
+//    ~20 G/s and ~170 G/s here, far below streaming).  A sort kernel reads
+//    tiles of 8192 positions (vals and columns), finds each position's row
+//    in an LDS copy of the tile's row starts, forms the contribution
+//    vals[p] * dy[row(p)] (and dvals), counts the tile per column bucket
+//    (2^k columns, about 256 buckets) in LDS, orders it by bucket in LDS and
+//    writes it out with the low column bits beside it, plus each bucket's
+//    segment offsets; one workgroup per bucket then sums its segments of
+//    every tile into an LDS copy of its dX slice (compare-and-swap float
+//    adds) and writes the slice once.  The order of the additions within a
+//    column varies between runs, as with the reference's atomics.  Column
+//    counts too large for 1024 buckets of 16384 columns fall back to
+//    zero-fill plus fp32 atomics from the walk.
 //  * D > 1 (SpMM): L lanes per row (L = 4, 16 or 64), float4 columns when
 //    D % 4 == 0 and X / Y are 16-byte aligned; the lanes of a row share each
 //    (col, val) load and read the X row coalesced.  Backward (K <= 16384):
@@ -409,14 +411,13 @@ __global__ __launch_bounds__(kThreads) void spmv_d1_fwd_kernel(
 }
 
 // ----------------------------------------------------------- D == 1 backward
-// Outputs per instantiation: dvals (DV), and for dX either nothing
-// (kNoDx), the per-position contributions vals[p] * dy[row(p)] in position
-// order (kContrib, summed by column afterwards), or fp32 atomics into a
-// zeroed dx (kAtomic, the fallback).
-constexpr int kNoDx = 0, kContrib = 1, kAtomic = 2;
+// Outputs per instantiation: dvals (DV), and for dX either nothing (kNoDx)
+// or fp32 atomics into a zeroed dx (kAtomic, the fallback beyond the bucket
+// sort's column limit).
+constexpr int kNoDx = 0, kAtomic = 1;
 
 // GX: x[col[p]] comes from xg (the forward's gathered copy) instead of a
-// gather, and col_idx is not read at all (MODE kNoDx or kContrib only).
+// gather, and col_idx is not read at all (MODE kNoDx only).
 template <typename I, bool VEC, bool DV, int MODE, bool GX>
 __device__ __forceinline__ void bwd_walk(const I* __restrict__ ptr, const I* __restrict__ col,
                                          const float* __restrict__ vals,
@@ -482,16 +483,6 @@ __device__ __forceinline__ void bwd_walk(const I* __restrict__ ptr, const I* __r
           if (in[j]) dvals[q0 + j] = g[j] * xv[j];
       }
     }
-    if constexpr (MODE == kContrib) {
-      if (VEC && full) {
-        *reinterpret_cast<f32x4*>(out + q0) =
-            f32x4{v[0] * g[0], v[1] * g[1], v[2] * g[2], v[3] * g[3]};
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (in[j]) out[q0 + j] = v[j] * g[j];
-      }
-    }
     if constexpr (MODE == kAtomic) {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
@@ -505,7 +496,7 @@ __device__ __forceinline__ void bwd_walk(const I* __restrict__ ptr, const I* __r
   }
 }
 
-// `out` is the contribution array (kContrib) or dx (kAtomic).
+// `out` is dx (kAtomic).
 template <typename I, bool VEC, bool DV, int MODE, bool GX>
 __global__ __launch_bounds__(kThreads) void spmv_d1_bwd_kernel(
     const I* __restrict__ ptr, const I* __restrict__ col, const float* __restrict__ vals,
@@ -533,8 +524,8 @@ __global__ __launch_bounds__(kThreads) void spmv_d1_bwd_kernel(
 
 // -------------------------------------------- D == 1 dX: bucket sort + sum
 constexpr int kSortThreads = 512;
-constexpr int kSortTile = 16384;                    // positions per sort workgroup
-constexpr int kSortPer = kSortTile / kSortThreads;  // 32 per thread, as 8 quads
+constexpr int kSortTile = 8192;                     // positions per sort workgroup
+constexpr int kSortPer = kSortTile / kSortThreads;  // 16 per thread, as 4 quads
 constexpr int kMaxBuckets = 1024;
 constexpr int kMaxBucketCols = 16384;               // LDS floats of one bucket's sums
 constexpr int kSumThreads = 1024;
@@ -566,122 +557,24 @@ __device__ __forceinline__ unsigned wave_incl_scan(unsigned v, int lane) {
   return v;
 }
 
-// Tile t = positions [16384 t, 16384 t + 16384): reads the contributions
-// (`val`) and columns, orders the tile by bucket (column >> shift) and
-// writes it back in place -- val[lo + i] and the low column bits lowcol[lo
-// + i] -- and meta[t * (nb + 1) + b] = absolute start of bucket b's segment
-// (meta[.. + nb] = end of the tile).  The whole tile is read into
-// registers before anything is written, and tiles are disjoint, so the
-// in-place write is safe.
-template <typename I, bool VEC>
-__global__ __launch_bounds__(kSortThreads) void spmv_bucket_sort_kernel(
-    const I* __restrict__ col, float* __restrict__ val, uint16_t* __restrict__ lowcol,
-    int64_t* __restrict__ meta, int64_t nnz, int64_t K, int shift, int nb) {
-  __shared__ float s_val[kSortTile];
-  __shared__ uint16_t s_low[kSortTile];
-  __shared__ unsigned s_cur[kMaxBuckets];
-  __shared__ unsigned s_wave[kSortThreads / 64];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t lo = (int64_t)blockIdx.x * kSortTile;
-  const int n = (int)min((int64_t)kSortTile, nnz - lo);
-  for (int b = tid; b < nb; b += kSortThreads) s_cur[b] = 0;
-
-  unsigned cc[kSortPer];
-  float vv[kSortPer];
-#pragma unroll
-  for (int g = 0; g < kSortPer / 4; ++g) {
-    const int i = 4 * (tid + kSortThreads * g);
-    if (VEC && i + 3 < n) {
-      const f32x4 v4 = *reinterpret_cast<const f32x4*>(val + lo + i);
-      int64_t c4[4];
-      if constexpr (sizeof(I) == 4) {
-        const i32x4_t ci = *reinterpret_cast<const i32x4_t*>(col + lo + i);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) c4[j] = ci[j];
-      } else {
-        const i64x2_t c0 = *reinterpret_cast<const i64x2_t*>(col + lo + i);
-        const i64x2_t c1 = *reinterpret_cast<const i64x2_t*>(col + lo + i + 2);
-        c4[0] = c0[0]; c4[1] = c0[1]; c4[2] = c1[0]; c4[3] = c1[1];
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        cc[4 * g + j] = (unsigned)(c4[j] < 0 ? 0 : (c4[j] >= K ? K - 1 : c4[j]));
-        vv[4 * g + j] = v4[j];
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const bool ok = i + j < n;
-        cc[4 * g + j] = ok ? (unsigned)ld_col(col, lo + i + j, K) : 0u;
-        vv[4 * g + j] = ok ? val[lo + i + j] : 0.f;
-      }
-    }
-  }
-  __syncthreads();  // s_cur zeroed
-#pragma unroll
-  for (int g = 0; g < kSortPer / 4; ++g)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (4 * (tid + kSortThreads * g) + j < n)
-        __hip_atomic_fetch_add(&s_cur[cc[4 * g + j] >> shift], 1u, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_WORKGROUP);
-  __syncthreads();
-
-  // Exclusive scan of the nb <= 1024 bucket counts, two per thread.
-  const int b0 = 2 * tid;
-  const unsigned a0 = b0 < nb ? s_cur[b0] : 0u;
-  const unsigned a1 = b0 + 1 < nb ? s_cur[b0 + 1] : 0u;
-  const unsigned incl = wave_incl_scan(a0 + a1, lane);
-  if (lane == 63) s_wave[wave] = incl;
-  __syncthreads();
-  unsigned off = incl - (a0 + a1);
-  for (int w = 0; w < wave; ++w) off += s_wave[w];
-  int64_t* mrow = meta + (int64_t)blockIdx.x * (nb + 1);
-  if (b0 < nb) {
-    s_cur[b0] = off;
-    mrow[b0] = lo + off;
-  }
-  if (b0 + 1 < nb) {
-    s_cur[b0 + 1] = off + a0;
-    mrow[b0 + 1] = lo + off + a0;
-  }
-  if (tid == 0) mrow[nb] = lo + n;
-  __syncthreads();
-
-  // Place: a bucket's cursor hands out the slots of its segment.
-  const unsigned low_mask = (1u << shift) - 1u;
-#pragma unroll
-  for (int g = 0; g < kSortPer / 4; ++g)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (4 * (tid + kSortThreads * g) + j < n) {
-        const unsigned c = cc[4 * g + j];
-        unsigned r = __hip_atomic_fetch_add(&s_cur[c >> shift], 1u, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_WORKGROUP);
-        r = r < (unsigned)kSortTile ? r : (unsigned)kSortTile - 1u;
-        s_val[r] = vv[4 * g + j];
-        s_low[r] = (uint16_t)(c & low_mask);
-      }
-  __syncthreads();
-
-  for (int i = 4 * tid; i < n; i += 4 * kSortThreads) {
-    if (i + 3 < n) {
-      *reinterpret_cast<f32x4*>(val + lo + i) = *reinterpret_cast<const f32x4*>(s_val + i);
-      *reinterpret_cast<uint2*>(lowcol + lo + i) = *reinterpret_cast<const uint2*>(s_low + i);
-    } else {
-      for (int j = i; j < n; ++j) {
-        val[lo + j] = s_val[j];
-        lowcol[lo + j] = s_low[j];
-      }
-    }
-  }
+// dx[b * cols, b * cols + cols) for bucket b: the bucket's segments of
+// every tile, summed in LDS.  A wave takes 64 tiles at a time and treats
+// their segments as one list (an exclusive prefix of the segment lengths in
+// LDS maps list entry e to its tile), so each lane loads kSumUnroll
+// independent entries per round.
+//
+// Workgroups go to the 8 XCDs round-robin (workgroup i to XCD i % 8), and a
+// segment's first and last cache lines are shared with the neighbouring
+// buckets' segments.  So each XCD takes a contiguous run of buckets: within
+// a tile their segments are one contiguous stretch, whose lines that XCD's
+// L2 fetches once.  (Bucket b = workgroup b put neighbours on different
+// XCDs, and each boundary line was fetched twice: 2.7 times the entries'
+// bytes came from HBM.)
+__device__ __forceinline__ int xcd_bucket(int i, int nb) {
+  const int q = nb >> 3, r = nb & 7, x = i & 7;
+  return x * q + min(x, r) + (i >> 3);
 }
 
-// dx[b * cols, b * cols + cols) for bucket b = blockIdx.x: the bucket's
-// segments of every tile, summed in LDS.  A wave takes 64 tiles at a time
-// and treats their segments as one list (an exclusive prefix of the segment
-// lengths in LDS maps list entry e to its tile), so each lane loads
-// kSumUnroll independent entries per round.
 __global__ __launch_bounds__(kSumThreads) void spmv_bucket_sum_kernel(
     const float* __restrict__ val, const uint16_t* __restrict__ lowcol,
     const int64_t* __restrict__ meta, int64_t n_tiles, int nb, int cols, int64_t K,
@@ -690,7 +583,7 @@ __global__ __launch_bounds__(kSumThreads) void spmv_bucket_sum_kernel(
   __shared__ int64_t s_start[kSumWaves][64];
   __shared__ int s_pre[kSumWaves][65];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int b = blockIdx.x;
+  const int b = xcd_bucket((int)blockIdx.x, nb);
   for (int i = tid; i < cols; i += kSumThreads) acc[i] = 0.f;
   __syncthreads();
   const int64_t n_groups = (n_tiles + 63) / 64;
@@ -709,18 +602,21 @@ __global__ __launch_bounds__(kSumThreads) void spmv_bucket_sum_kernel(
     if (lane == 63) s_pre[wave][64] = incl;
     const int E = __shfl(incl, 63, 64);
     __builtin_amdgcn_wave_barrier();
-    int j = 0;  // the lane's current tile; entries e grow, so j only advances
     for (int e0 = 0; e0 < E; e0 += 64 * kSumUnroll) {
       // Positions first (LDS only), then every global load without a branch
-      // between them, then the LDS additions.
+      // between them, then the LDS additions.  Entry e lies in tile j, the
+      // last with s_pre[j] <= e (a fixed six-step search, independent per
+      // entry, so the entries' searches overlap).
       int64_t pp[kSumUnroll];
       bool ok[kSumUnroll];
 #pragma unroll
       for (int u = 0; u < kSumUnroll; ++u) {
         const int e = e0 + 64 * u + lane;
         ok[u] = e < E;
-        const int ee = ok[u] ? e : E - 1;       // E - 1 >= every earlier e
-        while (s_pre[wave][j + 1] <= ee) ++j;   // stops: s_pre[wave][64] = E > ee
+        const int ee = ok[u] ? e : E - 1;
+        int j = 0;
+#pragma unroll
+        for (int step = 32; step > 0; step >>= 1) j += s_pre[wave][j + step] <= ee ? step : 0;
         pp[u] = s_start[wave][j] + (ee - s_pre[wave][j]);
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -1269,6 +1165,225 @@ __global__ __launch_bounds__(kThreads) void spmm_t_gather_kernel(
   }
 }
 
+// ------------------------------ D == 1 dX: contributions formed in the sort
+// Tile t = positions [kSortTile t, kSortTile (t + 1)): each position's
+// contribution vals[p] * dy[row(p)] -- and dvals[p] = dy[row(p)] *
+// x[col(p)], from the forward's gathered copy of x (kDvKept) or by
+// gathering x (kDvGather) -- ordered by bucket (column >> shift) and written
+// as val_out[lo + i] with the low column bits lowcol[lo + i], plus
+// meta[t * (nb + 1) + b] = absolute start of bucket b's segment (meta[.. +
+// nb] = end of the tile).  A position's row comes from an LDS copy of the
+// row starts inside the tile (a fixed-step search for a quad's first
+// position, forward steps for the other three); a tile spanning more rows
+// than the copy holds searches row_ptr in global memory.  Positions outside
+// [row_ptr[0], row_ptr[M]) belong to no row: they contribute zero and get
+// no dvals.
+// tile_rows[t] for t in [0, n_tiles]: the last row r with row_ptr[r] <=
+// min(t * kSortTile, nnz - 1), clamped into [0, M - 1] -- the row holding
+// sort tile t's first position, and (as entry t + 1) an upper bound on the
+// row holding its last.  One wave per entry.
+template <typename I>
+__global__ __launch_bounds__(kThreads) void spmv_tile_rows_kernel(const I* __restrict__ ptr,
+                                                                  int64_t* __restrict__ tile_rows,
+                                                                  int64_t M, int64_t nnz,
+                                                                  int64_t n_tiles) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (t > n_tiles) return;
+  const int64_t p = min(t * kSortTile, nnz - 1);
+  const int64_t r = rows_lower_bound(ptr, M, nnz, p + 1, lane, 0) - 1;
+  if (lane == 0) tile_rows[t] = max((int64_t)0, min(r, M - 1));
+}
+
+constexpr int kTileRowWin = 4096;  // row starts of a tile staged in LDS (within s_val)
+static_assert(kTileRowWin <= kSortTile, "the row starts share s_val's LDS");
+constexpr int kDvNone = 0, kDvKept = 1, kDvGather = 2;
+template <typename I, bool VEC, int DVM>
+__global__ __launch_bounds__(kSortThreads) void spmv_walk_sort_kernel(
+    const I* __restrict__ ptr, const I* __restrict__ col, const float* __restrict__ vals,
+    const float* __restrict__ x, const float* __restrict__ xg, const float* __restrict__ dy,
+    float* __restrict__ dvals, float* __restrict__ val_out, uint16_t* __restrict__ lowcol,
+    int64_t* __restrict__ meta, const int64_t* __restrict__ tile_rows, int64_t M, int64_t nnz,
+    int64_t K, int shift, int nb) {
+  __shared__ float s_val[kSortTile];
+  __shared__ uint16_t s_low[kSortTile];
+  __shared__ unsigned s_cur[kMaxBuckets];
+  __shared__ unsigned s_wave[kSortThreads / 64];
+  // row_ptr[ra + 1 + k] - lo, clamped into [0, kSortTile]: read before the
+  // first barrier of the counting step, s_val written after it
+  int* s_win = reinterpret_cast<int*>(s_val);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t lo = (int64_t)blockIdx.x * kSortTile;
+  const int n = (int)min((int64_t)kSortTile, nnz - lo);
+  for (int b = tid; b < nb; b += kSortThreads) s_cur[b] = 0;
+
+  // Structure loads first (branch-free: the vector form reads whole quads at
+  // clamped addresses, the scalar form clamps each position).
+  unsigned cc[kSortPer];
+  float vv[kSortPer], xv[kSortPer];
+#pragma unroll
+  for (int g = 0; g < kSortPer / 4; ++g) {
+    const int i = 4 * (tid + kSortThreads * g);
+    if (VEC && i + 3 < n) {
+      const f32x4 v4 = *reinterpret_cast<const f32x4*>(vals + lo + i);
+      f32x4 x4 = f32x4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (DVM == kDvKept) x4 = *reinterpret_cast<const f32x4*>(xg + lo + i);
+      int64_t c4[4];
+      if constexpr (sizeof(I) == 4) {
+        const i32x4_t ci = *reinterpret_cast<const i32x4_t*>(col + lo + i);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c4[j] = ci[j];
+      } else {
+        const i64x2_t c0 = *reinterpret_cast<const i64x2_t*>(col + lo + i);
+        const i64x2_t c1 = *reinterpret_cast<const i64x2_t*>(col + lo + i + 2);
+        c4[0] = c0[0]; c4[1] = c0[1]; c4[2] = c1[0]; c4[3] = c1[1];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        cc[4 * g + j] = (unsigned)(c4[j] < 0 ? 0 : (c4[j] >= K ? K - 1 : c4[j]));
+        vv[4 * g + j] = v4[j];
+        xv[4 * g + j] = x4[j];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t q = lo + min(i + j, n - 1);
+        cc[4 * g + j] = (unsigned)ld_col(col, q, K);
+        vv[4 * g + j] = vals[q];
+        if constexpr (DVM == kDvKept) xv[4 * g + j] = xg[q];
+        else xv[4 * g + j] = 0.f;
+      }
+    }
+  }
+  // the row holding the tile's first position, and an upper bound on the
+  // one holding its last (the row of the next tile's first position)
+  const int64_t ra = min(max(tile_rows[blockIdx.x], (int64_t)0), M - 1);
+  const int64_t rb = max(ra, min(tile_rows[blockIdx.x + 1], M - 1));
+  const int64_t p_first = ld_ptr(ptr, 0, nnz), p_end = ld_ptr(ptr, M, nnz);
+  // rows from the LDS copy when the tile's row starts fit it; entries past
+  // the copied ones hold a sentinel above every tile offset
+  const bool windowed = rb - ra < kTileRowWin;
+  const int nwin = windowed ? (int)(rb - ra) : 0;
+  if (windowed) {
+    for (int k = tid; k < kTileRowWin; k += kSortThreads) {
+      int v = kSortTile + 1;
+      if (k < nwin)
+        v = (int)min(max(ld_ptr(ptr, ra + 1 + k, nnz) - lo, (int64_t)0), (int64_t)kSortTile);
+      s_win[k] = v;
+    }
+  }
+  if constexpr (DVM == kDvGather) {
+#pragma unroll
+    for (int k = 0; k < kSortPer; ++k) xv[k] = x[cc[k]];
+  }
+  __syncthreads();  // s_win; s_cur zeroed
+
+  // Each position's row, then its contribution (and dvals).
+  float gy[kSortPer];
+#pragma unroll
+  for (int g = 0; g < kSortPer / 4; ++g) {
+    const int i0 = 4 * (tid + kSortThreads * g);
+    int64_t rid[4];
+    if (windowed) {
+      // a = the number of row starts at or before i0 (at most nwin <=
+      // kTileRowWin - 1): a fixed-step search, so the quads' searches
+      // interleave; the quad's other positions step forward from it
+      int a = 0;
+#pragma unroll
+      for (int step = kTileRowWin / 2; step > 0; step >>= 1)
+        a += s_win[a + step - 1] <= i0 ? step : 0;
+      rid[0] = ra + a;
+#pragma unroll
+      for (int j = 1; j < 4; ++j) {
+        while (s_win[a] <= i0 + j) ++a;
+        rid[j] = ra + a;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) rid[j] = row_of(ptr, ra, rb, lo + min(i0 + j, n - 1), nnz);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) gy[4 * g + j] = dy[min(max(rid[j], (int64_t)0), M - 1)];
+  }
+#pragma unroll
+  for (int g = 0; g < kSortPer / 4; ++g) {
+    const int i0 = 4 * (tid + kSortThreads * g);
+    bool in[4];
+    f32x4 dv;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t p = lo + i0 + j;
+      in[j] = i0 + j < n && p >= p_first && p < p_end;
+      const int k = 4 * g + j;
+      dv[j] = gy[k] * xv[k];
+      vv[k] = in[j] ? vv[k] * gy[k] : 0.f;
+    }
+    if constexpr (DVM != kDvNone) {
+      if (VEC && in[0] && in[1] && in[2] && in[3]) {
+        *reinterpret_cast<f32x4*>(dvals + lo + i0) = dv;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (in[j]) dvals[lo + i0 + j] = dv[j];
+      }
+    }
+  }
+
+  // Count per bucket, scan, place, write: as spmv_bucket_sort_kernel.
+#pragma unroll
+  for (int g = 0; g < kSortPer / 4; ++g)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (4 * (tid + kSortThreads * g) + j < n)
+        __hip_atomic_fetch_add(&s_cur[cc[4 * g + j] >> shift], 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
+  __syncthreads();
+  const int b0 = 2 * tid;
+  const unsigned a0 = b0 < nb ? s_cur[b0] : 0u;
+  const unsigned a1 = b0 + 1 < nb ? s_cur[b0 + 1] : 0u;
+  const unsigned incl = wave_incl_scan(a0 + a1, lane);
+  if (lane == 63) s_wave[wave] = incl;
+  __syncthreads();
+  unsigned off = incl - (a0 + a1);
+  for (int w = 0; w < wave; ++w) off += s_wave[w];
+  int64_t* mrow = meta + (int64_t)blockIdx.x * (nb + 1);
+  if (b0 < nb) {
+    s_cur[b0] = off;
+    mrow[b0] = lo + off;
+  }
+  if (b0 + 1 < nb) {
+    s_cur[b0 + 1] = off + a0;
+    mrow[b0 + 1] = lo + off + a0;
+  }
+  if (tid == 0) mrow[nb] = lo + n;
+  __syncthreads();
+  const unsigned low_mask = (1u << shift) - 1u;
+#pragma unroll
+  for (int g = 0; g < kSortPer / 4; ++g)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (4 * (tid + kSortThreads * g) + j < n) {
+        const unsigned c = cc[4 * g + j];
+        unsigned r = __hip_atomic_fetch_add(&s_cur[c >> shift], 1u, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_WORKGROUP);
+        r = r < (unsigned)kSortTile ? r : (unsigned)kSortTile - 1u;
+        s_val[r] = vv[4 * g + j];
+        s_low[r] = (uint16_t)(c & low_mask);
+      }
+  __syncthreads();
+  for (int i = 4 * tid; i < n; i += 4 * kSortThreads) {
+    if (i + 3 < n) {
+      *reinterpret_cast<f32x4*>(val_out + lo + i) = *reinterpret_cast<const f32x4*>(s_val + i);
+      *reinterpret_cast<uint2*>(lowcol + lo + i) = *reinterpret_cast<const uint2*>(s_low + i);
+    } else {
+      for (int j = i; j < n; ++j) {
+        val_out[lo + j] = s_val[j];
+        lowcol[lo + j] = s_low[j];
+      }
+    }
+  }
+}
+
 __global__ __launch_bounds__(kThreads) void spmv_fill_zero_kernel(float* __restrict__ a,
                                                                    int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
@@ -1346,7 +1461,7 @@ int forward(const I* ptr, const I* col, const float* vals, const float* X, float
   return nl2k::check_launch(who);
 }
 
-// Xg != nullptr (dvals requested, mode kContrib or kNoDx): the gathered walk.
+// Xg != nullptr (dvals requested, mode kNoDx): the gathered walk.
 template <typename I>
 void launch_d1_bwd(bool vec, bool dv, int mode, unsigned blocks, hipStream_t stream,
                    const I* ptr, const I* col, const float* vals, const float* X,
@@ -1355,18 +1470,12 @@ void launch_d1_bwd(bool vec, bool dv, int mode, unsigned blocks, hipStream_t str
 #define D1_BWD(V, DVV, MM, GG)                                                                   \
   hipLaunchKernelGGL((spmv_d1_bwd_kernel<I, V, DVV, MM, GG>), dim3(blocks), dim3(kThreads), 0, \
                      stream, ptr, col, vals, X, Xg, dY, dvals, out, M, K, nnz, n_waves)
-#define D1_BWD_MODE(V, DVV)                            \
-  if (mode == kContrib) D1_BWD(V, DVV, kContrib, false); \
-  else if (mode == kAtomic) D1_BWD(V, DVV, kAtomic, false); \
+#define D1_BWD_MODE(V, DVV)                              \
+  if (mode == kAtomic) D1_BWD(V, DVV, kAtomic, false); \
   else D1_BWD(V, DVV, kNoDx, false)
-  if (dv && Xg != nullptr && mode != kAtomic) {
-    if (vec) {
-      if (mode == kContrib) D1_BWD(true, true, kContrib, true);
-      else D1_BWD(true, true, kNoDx, true);
-    } else {
-      if (mode == kContrib) D1_BWD(false, true, kContrib, true);
-      else D1_BWD(false, true, kNoDx, true);
-    }
+  if (dv && Xg != nullptr && mode == kNoDx) {
+    if (vec) D1_BWD(true, true, kNoDx, true);
+    else D1_BWD(false, true, kNoDx, true);
     return;
   }
   if (vec) {
@@ -1385,7 +1494,7 @@ struct BucketPlan {
   bool use = false;
   int shift = 0, cols = 0, nb = 0;
   int64_t n_tiles = 0;
-  size_t off_low = 0, off_meta = 0, bytes = 0;
+  size_t off_low = 0, off_meta = 0, off_rows = 0, bytes = 0;
 };
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
@@ -1404,7 +1513,8 @@ BucketPlan bucket_plan(int64_t K, int64_t D, int64_t nnz) {
   p.n_tiles = nl2k::ceil_div(nnz, kSortTile);
   p.off_low = align256((size_t)nnz * sizeof(float));
   p.off_meta = p.off_low + align256((size_t)nnz * sizeof(uint16_t));
-  p.bytes = p.off_meta + (size_t)p.n_tiles * (size_t)(p.nb + 1) * sizeof(int64_t);
+  p.off_rows = p.off_meta + align256((size_t)p.n_tiles * (size_t)(p.nb + 1) * sizeof(int64_t));
+  p.bytes = p.off_rows + (size_t)(p.n_tiles + 1) * sizeof(int64_t);
   return p;
 }
 
@@ -1564,32 +1674,37 @@ int backward(const I* ptr, const I* col, const float* vals, const float* X, cons
   }
   // the walk gathers x for dvals unless it reads the gathered copy (the
   // atomic dX route, beyond the bucket limits, always gathers)
-  const bool gathers = dvals && !(Xg && (sorted_dx || !dX));
+  const bool gathers = dvals && !(Xg && !dX);
   const int64_t wave_items = gathers ? kWaveItemsShort : kWaveItemsLong;
   if (sorted_dx) {
-    const int64_t n_waves = std::max<int64_t>(1, nl2k::ceil_div(nnz + M, wave_items));
-    const int64_t blocks = nl2k::ceil_div(n_waves, kThreads / 64);
-    if (blocks > INT32_MAX || bp.n_tiles > INT32_MAX)
-      return nl2k::fail(NL2K_ERR_OVERFLOW, "%s: too many rows", who);
+    // one kernel per sort tile forms the contributions (and dvals) and
+    // sorts them by column bucket; one per bucket sums them into dx
+    if (bp.n_tiles > INT32_MAX) return nl2k::fail(NL2K_ERR_OVERFLOW, "%s: too many rows", who);
     char* ws = static_cast<char*>(workspace);
     float* contrib = reinterpret_cast<float*>(ws);
     uint16_t* low = reinterpret_cast<uint16_t*>(ws + bp.off_low);
     int64_t* meta = reinterpret_cast<int64_t*>(ws + bp.off_meta);
+    int64_t* tile_rows = reinterpret_cast<int64_t*>(ws + bp.off_rows);
+    hipLaunchKernelGGL((spmv_tile_rows_kernel<I>),
+                       dim3((unsigned)nl2k::ceil_div(bp.n_tiles + 1, kThreads / 64)),
+                       dim3(kThreads), 0, stream, ptr, tile_rows, M, nnz, bp.n_tiles);
+    st = nl2k::check_launch(who);
+    if (st) return st;
     const bool vec = nl2k::aligned16(col) && nl2k::aligned16(vals) &&
                      (dvals == nullptr || nl2k::aligned16(dvals)) &&
                      (Xg == nullptr || nl2k::aligned16(Xg));
-    launch_d1_bwd<I>(vec, dvals != nullptr, kContrib, (unsigned)blocks, stream, ptr, col, vals,
-                     X, Xg, dY, dvals, contrib, M, K, nnz, n_waves);
-    st = nl2k::check_launch(who);
-    if (st) return st;
-    if (nl2k::aligned16(col))
-      hipLaunchKernelGGL((spmv_bucket_sort_kernel<I, true>), dim3((unsigned)bp.n_tiles),
-                         dim3(kSortThreads), 0, stream, col, contrib, low, meta, nnz, K, bp.shift,
-                         bp.nb);
-    else
-      hipLaunchKernelGGL((spmv_bucket_sort_kernel<I, false>), dim3((unsigned)bp.n_tiles),
-                         dim3(kSortThreads), 0, stream, col, contrib, low, meta, nnz, K, bp.shift,
-                         bp.nb);
+    const int dvm = dvals == nullptr ? kDvNone : (Xg != nullptr ? kDvKept : kDvGather);
+#define WALK_SORT(VV, DD)                                                                    \
+  hipLaunchKernelGGL((spmv_walk_sort_kernel<I, VV, DD>), dim3((unsigned)bp.n_tiles),       \
+                     dim3(kSortThreads), 0, stream, ptr, col, vals, X, Xg, dY, dvals, contrib, \
+                     low, meta, tile_rows, M, nnz, K, bp.shift, bp.nb)
+#define WALK_SORT_DV(VV)                          \
+  if (dvm == kDvNone) WALK_SORT(VV, kDvNone);     \
+  else if (dvm == kDvKept) WALK_SORT(VV, kDvKept); \
+  else WALK_SORT(VV, kDvGather)
+    if (vec) { WALK_SORT_DV(true); } else { WALK_SORT_DV(false); }
+#undef WALK_SORT_DV
+#undef WALK_SORT
     st = nl2k::check_launch(who);
     if (st) return st;
     hipLaunchKernelGGL(spmv_bucket_sum_kernel, dim3((unsigned)bp.nb), dim3(kSumThreads), 0,

@@ -185,13 +185,15 @@ def test_spmv_argument_validation_without_gpu():
     assert st == STATUS["NL2K_ERR_NULL"]
     assert lib.spmv_forward_f32_i32(fake, fake, fake, fake, fake, 0, 4, 1, 0, None) == 0
     # dX at D == 1 is summed by column bucket in a workspace: contributions
-    # (4 B) and low column bits (2 B) per nonzero, each 256-byte aligned, then
-    # nb + 1 int64 segment offsets per 16384-position tile; 2^20 columns ->
-    # 256 buckets of 4096
+    # (4 B) and low column bits (2 B) per nonzero, then nb + 1 int64 segment
+    # offsets per 8192-position tile, each 256-byte aligned, then one int64
+    # row per tile boundary; 2^20 columns -> 256 buckets of 4096
     nnz, K = 16 * 2**20, 2**20
-    tiles = nnz // 16384
-    assert lib.spmv_backward_workspace_bytes(K, K, 1, nnz) == 4 * nnz + 2 * nnz + tiles * 257 * 8
-    assert lib.spmv_backward_workspace_bytes(100, 7, 1, 10) == 256 + 256 + 1 * 2 * 8  # 1 bucket
+    tiles = nnz // 8192
+    assert lib.spmv_backward_workspace_bytes(K, K, 1, nnz) == (
+        4 * nnz + 2 * nnz + tiles * 257 * 8 + (tiles + 1) * 8)
+    # 1 bucket, 1 tile
+    assert lib.spmv_backward_workspace_bytes(100, 7, 1, 10) == 256 + 256 + 256 + 2 * 8
     assert lib.spmv_backward_workspace_bytes(K, K, 64, nnz) == 0  # D > 1, K > 16384: atomics
     # D > 1 with K <= 16384: the column-major copy of A (trip counter and look-back
     # slots first, then chunk offsets, colptr, 16-byte {row, position, value} records)
