@@ -1329,7 +1329,10 @@ __global__ __launch_bounds__(kSortThreads) void spmv_walk_sort_kernel(
     }
   }
 
-  // Count per bucket, scan, place, write: as spmv_bucket_sort_kernel.
+  // Count per bucket (LDS integer atomics), exclusive scan of the counts
+  // (two buckets per thread), then place: a bucket's cursor hands out the
+  // slots of its segment, so the tile is ordered by bucket in LDS before it
+  // is written out with 16-byte stores.
 #pragma unroll
   for (int g = 0; g < kSortPer / 4; ++g)
 #pragma unroll
