@@ -1195,6 +1195,14 @@ __global__ __launch_bounds__(kThreads) void spmv_tile_rows_kernel(const I* __res
   if (lane == 0) tile_rows[t] = max((int64_t)0, min(r, M - 1));
 }
 
+// base + a 32-bit byte offset: the load or store takes the base from scalar
+// registers and the offset from one vector register (no 64-bit address math)
+template <typename T>
+__device__ __forceinline__ T* at_byte(T* base, unsigned off) {
+  using C = std::conditional_t<std::is_const<T>::value, const char, char>;
+  return reinterpret_cast<T*>(reinterpret_cast<C*>(base) + off);
+}
+
 constexpr int kTileRowWin = 4096;  // row starts of a tile staged in LDS (within s_val)
 static_assert(kTileRowWin <= kSortTile, "the row starts share s_val's LDS");
 constexpr int kDvNone = 0, kDvKept = 1, kDvGather = 2;
@@ -1215,95 +1223,123 @@ __global__ __launch_bounds__(kSortThreads) void spmv_walk_sort_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t lo = (int64_t)blockIdx.x * kSortTile;
   const int n = (int)min((int64_t)kSortTile, nnz - lo);
+  // Tile bases: every per-position index below is a 32-bit offset from one
+  // of these (a scalar base plus a vector offset, no 64-bit address math).
+  const I* __restrict__ ct = col + lo;
+  const float* __restrict__ vt = vals + lo;
+  const float* __restrict__ xt = xg + (DVM == kDvKept ? lo : 0);
+  float* __restrict__ dvt = dvals + (DVM != kDvNone ? lo : 0);
   for (int b = tid; b < nb; b += kSortThreads) s_cur[b] = 0;
+  // columns clamp into [0, K - 1]; the bucket plan keeps K at most 2^24
+  const int kmax = (int)(K - 1);
+  auto clamp_col = [&](auto c) -> unsigned {
+    return (unsigned)(c < 0 ? 0 : (c > (decltype(c))kmax ? kmax : (int)c));
+  };
 
-  // Structure loads first (branch-free: the vector form reads whole quads at
-  // clamped addresses, the scalar form clamps each position).
-  unsigned cc[kSortPer];
+  // Structure loads first, raw: one uniform branch picks whole-quad vector
+  // loads (tiles of a multiple of 4 positions) or clamped scalar loads, and
+  // nothing inside it reads a loaded value, so no wait separates the quads'
+  // loads (the columns are clamped after the row-start loads are issued).
+  I craw[kSortPer];
   float vv[kSortPer], xv[kSortPer];
+  if (VEC && (n & 3) == 0) {
 #pragma unroll
-  for (int g = 0; g < kSortPer / 4; ++g) {
-    const int i = 4 * (tid + kSortThreads * g);
-    if (VEC && i + 3 < n) {
-      const f32x4 v4 = *reinterpret_cast<const f32x4*>(vals + lo + i);
+    for (int g = 0; g < kSortPer / 4; ++g) {
+      const unsigned i = min(4u * (unsigned)(tid + kSortThreads * g), (unsigned)n - 4u);
+      const f32x4 v4 = *reinterpret_cast<const f32x4*>(at_byte(vt, 4u * i));
       f32x4 x4 = f32x4{0.f, 0.f, 0.f, 0.f};
-      if constexpr (DVM == kDvKept) x4 = *reinterpret_cast<const f32x4*>(xg + lo + i);
-      int64_t c4[4];
+      if constexpr (DVM == kDvKept) x4 = *reinterpret_cast<const f32x4*>(at_byte(xt, 4u * i));
       if constexpr (sizeof(I) == 4) {
-        const i32x4_t ci = *reinterpret_cast<const i32x4_t*>(col + lo + i);
+        const i32x4_t ci = *reinterpret_cast<const i32x4_t*>(at_byte(ct, 4u * i));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) c4[j] = ci[j];
+        for (int j = 0; j < 4; ++j) craw[4 * g + j] = ci[j];
       } else {
-        const i64x2_t c0 = *reinterpret_cast<const i64x2_t*>(col + lo + i);
-        const i64x2_t c1 = *reinterpret_cast<const i64x2_t*>(col + lo + i + 2);
-        c4[0] = c0[0]; c4[1] = c0[1]; c4[2] = c1[0]; c4[3] = c1[1];
+        const i64x2_t c0 = *reinterpret_cast<const i64x2_t*>(at_byte(ct, 8u * i));
+        const i64x2_t c1 = *reinterpret_cast<const i64x2_t*>(at_byte(ct, 8u * i + 16u));
+        craw[4 * g + 0] = c0[0];
+        craw[4 * g + 1] = c0[1];
+        craw[4 * g + 2] = c1[0];
+        craw[4 * g + 3] = c1[1];
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        cc[4 * g + j] = (unsigned)(c4[j] < 0 ? 0 : (c4[j] >= K ? K - 1 : c4[j]));
         vv[4 * g + j] = v4[j];
         xv[4 * g + j] = x4[j];
       }
-    } else {
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < kSortPer / 4; ++g)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int64_t q = lo + min(i + j, n - 1);
-        cc[4 * g + j] = (unsigned)ld_col(col, q, K);
-        vv[4 * g + j] = vals[q];
-        if constexpr (DVM == kDvKept) xv[4 * g + j] = xg[q];
+        const unsigned q = min(4u * (unsigned)(tid + kSortThreads * g) + j, (unsigned)n - 1u);
+        craw[4 * g + j] = *at_byte(ct, q * (unsigned)sizeof(I));
+        vv[4 * g + j] = *at_byte(vt, 4u * q);
+        if constexpr (DVM == kDvKept) xv[4 * g + j] = *at_byte(xt, 4u * q);
         else xv[4 * g + j] = 0.f;
       }
-    }
   }
   // the row holding the tile's first position, and an upper bound on the
   // one holding its last (the row of the next tile's first position)
   const int64_t ra = min(max(tile_rows[blockIdx.x], (int64_t)0), M - 1);
   const int64_t rb = max(ra, min(tile_rows[blockIdx.x + 1], M - 1));
-  const int64_t p_first = ld_ptr(ptr, 0, nnz), p_end = ld_ptr(ptr, M, nnz);
+  // positions [first_rel, end_rel) of the tile belong to rows
+  const int first_rel = (int)min(max(ld_ptr(ptr, 0, nnz) - lo, (int64_t)0), (int64_t)n);
+  const int end_rel = (int)min(max(ld_ptr(ptr, M, nnz) - lo, (int64_t)0), (int64_t)n);
   // rows from the LDS copy when the tile's row starts fit it; entries past
   // the copied ones hold a sentinel above every tile offset
   const bool windowed = rb - ra < kTileRowWin;
   const int nwin = windowed ? (int)(rb - ra) : 0;
-  if (windowed) {
-    for (int k = tid; k < kTileRowWin; k += kSortThreads) {
-      int v = kSortTile + 1;
-      if (k < nwin)
-        v = (int)min(max(ld_ptr(ptr, ra + 1 + k, nnz) - lo, (int64_t)0), (int64_t)kSortTile);
-      s_win[k] = v;
-    }
-  }
-  if constexpr (DVM == kDvGather) {
+  // (loaded and written without branches, also when unused: indices clamp
+  // in range, row_ptr[ra + 1] exists since ra <= M - 1)
+  constexpr int kPerThread = kTileRowWin / kSortThreads;
+  const I* __restrict__ pt = ptr + ra + 1;
+  const unsigned last = (unsigned)max(nwin - 1, 0);
+  I wraw[kPerThread];
 #pragma unroll
-    for (int k = 0; k < kSortPer; ++k) xv[k] = x[cc[k]];
+  for (int u = 0; u < kPerThread; ++u)
+    wraw[u] = *at_byte(pt, min((unsigned)(tid + kSortThreads * u), last) * (unsigned)sizeof(I));
+  unsigned cc[kSortPer];
+#pragma unroll
+  for (int k = 0; k < kSortPer; ++k) cc[k] = clamp_col(craw[k]);
+#pragma unroll
+  for (int u = 0; u < kPerThread; ++u) {
+    const int k = tid + kSortThreads * u;
+    const int v = (int)min(max((int64_t)wraw[u] - lo, (int64_t)0), (int64_t)kSortTile);
+    s_win[k] = k < nwin ? v : kSortTile + 1;
   }
   __syncthreads();  // s_win; s_cur zeroed
+  if constexpr (DVM == kDvGather) {
+#pragma unroll
+    for (int k = 0; k < kSortPer; ++k) xv[k] = *at_byte(x, 4u * cc[k]);
+  }
 
   // Each position's row, then its contribution (and dvals).
+  const float* __restrict__ dyt = dy + ra;
   float gy[kSortPer];
 #pragma unroll
   for (int g = 0; g < kSortPer / 4; ++g) {
     const int i0 = 4 * (tid + kSortThreads * g);
-    int64_t rid[4];
     if (windowed) {
       // a = the number of row starts at or before i0 (at most nwin <=
       // kTileRowWin - 1): a fixed-step search, so the quads' searches
-      // interleave; the quad's other positions step forward from it
-      int a = 0;
+      // interleave; the quad's other positions step forward from it.  Row
+      // ra + a lies in [ra, rb].
+      unsigned a = 0;
 #pragma unroll
-      for (int step = kTileRowWin / 2; step > 0; step >>= 1)
-        a += s_win[a + step - 1] <= i0 ? step : 0;
-      rid[0] = ra + a;
+      for (unsigned step = kTileRowWin / 2; step > 0; step >>= 1)
+        a += s_win[a + step - 1] <= i0 ? step : 0u;
+      gy[4 * g] = *at_byte(dyt, 4u * a);
 #pragma unroll
       for (int j = 1; j < 4; ++j) {
         while (s_win[a] <= i0 + j) ++a;
-        rid[j] = ra + a;
+        gy[4 * g + j] = *at_byte(dyt, 4u * a);
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) rid[j] = row_of(ptr, ra, rb, lo + min(i0 + j, n - 1), nnz);
+      for (int j = 0; j < 4; ++j)
+        gy[4 * g + j] = dy[row_of(ptr, ra, rb, lo + min(i0 + j, n - 1), nnz)];
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) gy[4 * g + j] = dy[min(max(rid[j], (int64_t)0), M - 1)];
   }
 #pragma unroll
   for (int g = 0; g < kSortPer / 4; ++g) {
@@ -1312,19 +1348,18 @@ __global__ __launch_bounds__(kSortThreads) void spmv_walk_sort_kernel(
     f32x4 dv;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int64_t p = lo + i0 + j;
-      in[j] = i0 + j < n && p >= p_first && p < p_end;
+      in[j] = i0 + j >= first_rel && i0 + j < end_rel;
       const int k = 4 * g + j;
       dv[j] = gy[k] * xv[k];
       vv[k] = in[j] ? vv[k] * gy[k] : 0.f;
     }
     if constexpr (DVM != kDvNone) {
       if (VEC && in[0] && in[1] && in[2] && in[3]) {
-        *reinterpret_cast<f32x4*>(dvals + lo + i0) = dv;
+        *reinterpret_cast<f32x4*>(at_byte(dvt, 4u * i0)) = dv;
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          if (in[j]) dvals[lo + i0 + j] = dv[j];
+          if (in[j]) *at_byte(dvt, 4u * (i0 + j)) = dv[j];
       }
     }
   }
@@ -1374,14 +1409,16 @@ __global__ __launch_bounds__(kSortThreads) void spmv_walk_sort_kernel(
         s_low[r] = (uint16_t)(c & low_mask);
       }
   __syncthreads();
+  float* __restrict__ vo = val_out + lo;
+  uint16_t* __restrict__ lw = lowcol + lo;
   for (int i = 4 * tid; i < n; i += 4 * kSortThreads) {
     if (i + 3 < n) {
-      *reinterpret_cast<f32x4*>(val_out + lo + i) = *reinterpret_cast<const f32x4*>(s_val + i);
-      *reinterpret_cast<uint2*>(lowcol + lo + i) = *reinterpret_cast<const uint2*>(s_low + i);
+      *reinterpret_cast<f32x4*>(at_byte(vo, 4u * i)) = *reinterpret_cast<const f32x4*>(s_val + i);
+      *reinterpret_cast<uint2*>(at_byte(lw, 2u * i)) = *reinterpret_cast<const uint2*>(s_low + i);
     } else {
       for (int j = i; j < n; ++j) {
-        val_out[lo + j] = s_val[j];
-        lowcol[lo + j] = s_low[j];
+        *at_byte(vo, 4u * j) = s_val[j];
+        *at_byte(lw, 2u * j) = s_low[j];
       }
     }
   }
