@@ -197,6 +197,17 @@ def test_spmv_structures(kind, m, k, d):
         _check(*_csr(lens, k, d, m + d, idx))
 
 
+def test_spmv_d1_beyond_the_bucket_sort():
+    """More columns than the bucket sort covers (1024 buckets of 16384
+    columns, 2^24): dX at D == 1 takes the zero-fill plus fp32 atomics route
+    from the walk, with and without the kept copy of X[col]."""
+    k = (1 << 24) + 4099
+    announce(f"spmv D=1 K={k} (atomic dX route)")
+    lens = np.random.default_rng(21).integers(0, 40, 800)
+    for idx in (torch.int32, torch.int64):
+        _check(*_csr(lens, k, 1, 21, idx))
+
+
 def test_spmv_no_nonzeros():
     announce("spmv nnz = 0")
     from cases.spmv import op
