@@ -49,6 +49,7 @@ __device__ __forceinline__ float inv_norm(float sumsq, float eps) {
 struct CosFwdOp {
   float eps;
   static constexpr bool kSideOut = true;
+  static constexpr bool kRowScales = true;
   __device__ __forceinline__ float row(f32x4 (&x)[4], float sx) const {
     const float s = inv_norm(sx, eps);
 #pragma unroll

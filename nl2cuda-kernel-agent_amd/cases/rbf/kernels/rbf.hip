@@ -58,6 +58,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 struct RbfFwdOp {
   float neg_kappa;  // -gamma log2(e)
   static constexpr bool kSideOut = false;
+  static constexpr bool kRowScales = false;
   __device__ __forceinline__ float row(f32x4 (&)[4], float sx) const { return neg_kappa * sx; }
   __device__ __forceinline__ float col(f32x4&, float sy) const { return sy; }
   __device__ __forceinline__ float out(float dot, float rt, float ct) const {

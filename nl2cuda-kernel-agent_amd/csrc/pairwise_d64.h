@@ -48,6 +48,8 @@ constexpr int64_t kMaxTileDim = INT32_MAX - 1024;
 // Op interface:
 //   static constexpr bool kSideOut      write Op::row / Op::col results to
 //                                       rowv [N] / colv [M] (once each)
+//   static constexpr bool kRowScales    Op::row rewrites the X row (it must
+//                                       then run before the row's MFMAs)
 //   float row(f32x4 (&x)[4], float sx)  row prep (x: this lane's 16 values
 //                                       of the row, sx = |x|^2); returns the
 //                                       row's epilogue term
@@ -99,17 +101,23 @@ __global__ __launch_bounds__(256, 2) void pair_fwd_d64_kernel(
 
   // X operand registers: lane (n, h) holds elements k = 16q + 4h + u of row
   // 16 ib + n of this wave's strip.  Contraction step (q, u) uses k-slot h.
+  // The loads go out q-major, so the first contraction steps wait only for
+  // their own slices.
   f32x4 xb[4][4];
   float ax[4];  // Op::row term of row 16 ib + n
   int cur_rb = -1;
   auto load_x = [&](int rb) {
     const int i0 = rb * kFwdRows + wave * 64;
 #pragma unroll
-    for (int ib = 0; ib < 4; ++ib) {
-      const int ir = min(i0 + ib * 16 + n, N - 1);
+    for (int q = 0; q < 4; ++q)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) xb[ib][q] = load4(X + (size_t)ir * kD + 16 * q + 4 * h);
-    }
+      for (int ib = 0; ib < 4; ++ib) {
+        const int ir = min(i0 + ib * 16 + n, N - 1);
+        xb[ib][q] = load4(X + (size_t)ir * kD + 16 * q + 4 * h);
+      }
+    cur_rb = rb;
+  };
+  auto row_terms = [&]() {
 #pragma unroll
     for (int ib = 0; ib < 4; ++ib) {
       float sx = 0.f;
@@ -121,11 +129,16 @@ __global__ __launch_bounds__(256, 2) void pair_fwd_d64_kernel(
       sx += __shfl_xor(sx, 32, 64);
       ax[ib] = op.row(xb[ib], sx);
     }
-    cur_rb = rb;
   };
 
-  load_x(u_begin / n_jt);
+  // Prologue: the Y tile's loads go out first, so staging it (and the
+  // barrier) waits for them alone, not for the X rows behind them; a row
+  // term that leaves the row unchanged is taken after the unit's MFMAs,
+  // which then wait only for the X slices they use.
   load_y(u_begin);
+  load_x(u_begin / n_jt);
+  if constexpr (Op::kRowScales) row_terms();
+  bool terms_due = !Op::kRowScales;
   commit_y(0);
   __syncthreads();
   int buf = 0;
@@ -163,6 +176,10 @@ __global__ __launch_bounds__(256, 2) void pair_fwd_d64_kernel(
       __builtin_amdgcn_sched_barrier(0);
     }
 
+    if (!Op::kRowScales && terms_due) {
+      row_terms();
+      terms_due = false;
+    }
     // Epilogue: out[i][j..j+3], i = i0 + 16 ib + n, j = j0 + 16 jb + 4h.
     const int i0 = (u / n_jt) * kFwdRows + wave * 64;
     const int j0 = (u % n_jt) * kTile;
@@ -205,7 +222,11 @@ __global__ __launch_bounds__(256, 2) void pair_fwd_d64_kernel(
     if (has_next) commit_y(buf ^ 1);
     __syncthreads();
     buf ^= 1;
-    if (has_next && (u + 1) / n_jt != cur_rb) load_x((u + 1) / n_jt);
+    if (has_next && (u + 1) / n_jt != cur_rb) {
+      load_x((u + 1) / n_jt);
+      if constexpr (Op::kRowScales) row_terms();
+      else terms_due = true;
+    }
   }
 }
 
