@@ -1166,18 +1166,6 @@ __global__ __launch_bounds__(kThreads) void spmm_t_gather_kernel(
 }
 
 // ------------------------------ D == 1 dX: contributions formed in the sort
-// Tile t = positions [kSortTile t, kSortTile (t + 1)): each position's
-// contribution vals[p] * dy[row(p)] -- and dvals[p] = dy[row(p)] *
-// x[col(p)], from the forward's gathered copy of x (kDvKept) or by
-// gathering x (kDvGather) -- ordered by bucket (column >> shift) and written
-// as val_out[lo + i] with the low column bits lowcol[lo + i], plus
-// meta[t * (nb + 1) + b] = absolute start of bucket b's segment (meta[.. +
-// nb] = end of the tile).  A position's row comes from an LDS copy of the
-// row starts inside the tile (a fixed-step search for a quad's first
-// position, forward steps for the other three); a tile spanning more rows
-// than the copy holds searches row_ptr in global memory.  Positions outside
-// [row_ptr[0], row_ptr[M]) belong to no row: they contribute zero and get
-// no dvals.
 // tile_rows[t] for t in [0, n_tiles]: the last row r with row_ptr[r] <=
 // min(t * kSortTile, nnz - 1), clamped into [0, M - 1] -- the row holding
 // sort tile t's first position, and (as entry t + 1) an upper bound on the
@@ -1203,6 +1191,18 @@ __device__ __forceinline__ T* at_byte(T* base, unsigned off) {
   return reinterpret_cast<T*>(reinterpret_cast<C*>(base) + off);
 }
 
+// Sort tile t = positions [kSortTile t, kSortTile (t + 1)): each position's
+// contribution vals[p] * dy[row(p)] -- and dvals[p] = dy[row(p)] *
+// x[col(p)], from the forward's gathered copy of x (kDvKept) or by
+// gathering x (kDvGather) -- ordered by bucket (column >> shift) and written
+// as val_out[lo + i] with the low column bits lowcol[lo + i], plus
+// meta[t * (nb + 1) + b] = absolute start of bucket b's segment (meta[.. +
+// nb] = end of the tile).  A position's row comes from an LDS copy of the
+// row starts inside the tile (a fixed-step search for a quad's first
+// position, forward steps for the other three); a tile spanning more rows
+// than the copy holds searches row_ptr in global memory.  Positions outside
+// [row_ptr[0], row_ptr[M]) belong to no row: they contribute zero and get
+// no dvals.
 constexpr int kTileRowWin = 4096;  // row starts of a tile staged in LDS (within s_val)
 static_assert(kTileRowWin <= kSortTile, "the row starts share s_val's LDS");
 constexpr int kDvNone = 0, kDvKept = 1, kDvGather = 2;
