@@ -179,6 +179,14 @@ def _lens(kind, m, k, rng):
         return lens
     if kind == "zipf":
         return np.minimum(rng.zipf(1.5, m), k)
+    if kind == "sparse_rows":  # rows of 0-1 nonzeros: sort tiles span more rows than their LDS copy
+        return (rng.random(m) < 0.15).astype(np.int64)
+    if kind == "tile_edges":  # rows starting on 8192-position sort-tile edges, empty ones too
+        lens = np.full(m, 8, np.int64)
+        lens[1024] = 0  # rows 1024 and 1025 both start at position 8192
+        lens[3000] = 13  # later edges fall inside rows
+        lens[5000:5003] = 0
+        return lens
     raise ValueError(kind)
 
 
@@ -188,7 +196,8 @@ def _lens(kind, m, k, rng):
     ("small", 4000, 1, 1), ("small", 1, 10, 1), ("small", 500, 300, 3), ("small", 500, 300, 4),
     ("zipf", 300, 200, 17), ("zipf", 300, 200, 64), ("small", 100, 100, 100),
     ("small", 100, 50, 256), ("one_long", 64, 64, 300), ("ends_only", 700, 90, 8),
-    ("small", 300, 20000, 4), ("small", 300, 16384, 8), ("mostly_empty", 2000, 1500, 32), ("one_long", 50, 3000, 16)])
+    ("small", 300, 20000, 4), ("small", 300, 16384, 8), ("mostly_empty", 2000, 1500, 32), ("one_long", 50, 3000, 16),
+    ("sparse_rows", 200000, 5000, 1), ("tile_edges", 6000, 3000, 1)])
 def test_spmv_structures(kind, m, k, d):
     announce(f"spmv {kind} M={m} K={k} D={d}")
     rng = np.random.default_rng(m + k + d)
