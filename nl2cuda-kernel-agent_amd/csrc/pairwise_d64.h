@@ -137,9 +137,9 @@ __global__ __launch_bounds__(256, 2) void pair_fwd_d64_kernel(
   // which then wait only for the X slices they use.
   load_y(u_begin);
   load_x(u_begin / n_jt);
+  commit_y(0);
   if constexpr (Op::kRowScales) row_terms();
   bool terms_due = !Op::kRowScales;
-  commit_y(0);
   __syncthreads();
   int buf = 0;
 
