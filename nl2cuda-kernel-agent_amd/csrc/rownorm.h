@@ -44,7 +44,6 @@ namespace rownorm {
 
 constexpr int kBlock = 256;
 constexpr int kBwdBlocks = 512;       // row-cached backward blocks = partial rows of dw / dbias
-constexpr int kBwdBlocksWide = 256;   // the same for rows of 4096 floats or more
 constexpr int kColsumWaves = 16;      // waves of a column-sum workgroup (64 columns)
 constexpr int kGenericMaxSplit = 512; // partial rows of the generic path
 
@@ -422,9 +421,7 @@ inline Plan plan(int64_t B, int64_t D, bool aligned) {
       p.tpr = 256;
       p.v = d4 <= 512 ? 2 : d4 <= 1024 ? 4 : 8;
     }
-    // Wide rows keep enough bytes in flight with fewer blocks, and fewer
-    // blocks mean fewer partial rows to write and sum.
-    p.rpb = std::max<int64_t>(1, ceil_div(B, D >= 4096 ? kBwdBlocksWide : kBwdBlocks));
+    p.rpb = std::max<int64_t>(1, ceil_div(B, kBwdBlocks));
   } else {
     // ~2048 blocks of 64 columns x (B / S1) rows
     const int64_t slices = ceil_div(D, 64);
