@@ -41,7 +41,6 @@
 //    reuse the captured nonce, never read an earlier replay's slots.
 //  * Reverse scans mirror the positions: logical p <-> physical D - 1 - p.
 #include <algorithm>
-#include <atomic>
 #include <cstdint>
 
 #include "../../../csrc/common.h"
@@ -379,36 +378,6 @@ int64_t launch_grid(const Plan& p, int64_t resident) {
   return std::max<int64_t>(1, std::min<int64_t>(p.total, resident));
 }
 
-// Resident workgroups of scan_rows_kernel<...> on the current device: CU
-// count x the occupancy the runtime computes for this kernel (registers, LDS
-// and launch bounds), cached per device and instantiation.
-template <typename K>
-int resident_blocks(K kernel, int* out) {
-  constexpr int kMaxDevices = 64;
-  static std::atomic<int> cache[kMaxDevices];
-  int dev = 0;
-  int st = nl2k::check_hip(hipGetDevice(&dev), "hipGetDevice");
-  if (st) return st;
-  if (dev >= 0 && dev < kMaxDevices) {
-    const int c = cache[dev].load(std::memory_order_relaxed);
-    if (c > 0) {
-      *out = c;
-      return NL2K_SUCCESS;
-    }
-  }
-  int cus = 0, per_cu = 0;
-  st = nl2k::check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev),
-                       "hipDeviceGetAttribute(MultiprocessorCount)");
-  if (st) return st;
-  st = nl2k::check_hip(
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, 0),
-      "hipOccupancyMaxActiveBlocksPerMultiprocessor");
-  if (st) return st;
-  const int n = std::max(1, cus) * std::max(1, per_cu);
-  if (dev >= 0 && dev < kMaxDevices) cache[dev].store(n, std::memory_order_relaxed);
-  *out = n;
-  return NL2K_SUCCESS;
-}
 
 
 int validate(int64_t rows, int64_t D, const char* who) {
@@ -448,7 +417,9 @@ int run(const In* x, Out* y, int64_t rows, int64_t D, void* workspace, size_t ws
                      : &scan_rows_kernel<In, Out, Acc, REV, false>;
   int resident = 1;
   if (p.nchunk > 1) {
-    st = resident_blocks(kernel, &resident);
+    // the grid stays within what the device holds at once (per device and
+    // instantiation), so every chunk's predecessors are running or done
+    st = nl2k::resident_blocks(reinterpret_cast<const void*>(kernel), kThreads, &resident);
     if (st) return st;
     hipError_t qe = hipSuccess;
     const bool cap = nl2k::slots::capturing(stream, &qe);

@@ -11,11 +11,12 @@
 //  * D == 1 (SpMV), power-law rows: rows are split between waves by the
 //    merge-path coordinate f(r) = row_ptr[r] + r, so every wave gets about S
 //    rows-plus-nonzeros and owns its rows outright (no cross-wave carries,
-//    no atomics, deterministic).  A wave finds its first row with a
+//    no atomics, deterministic); S is chosen so that the launch is one round
+//    of the waves the device holds at once.  A wave finds its first row with a
 //    64-way parallel search (four dependent probes at M = 2^20), then walks
 //    its nonzeros in steps of 256: lane l loads positions 4l..4l+3 with one
 //    16-byte load of col_idx and one of vals, gathers x, and finds each
-//    position's row by binary search over the next 256 row starts staged in
+//    position's row by binary search over the next 512 row starts staged in
 //    a wave-private LDS slice.  Per step: a serial sum over each lane's four
 //    products by row, a wave64 segmented inclusive scan (key = row) of the
 //    lanes' trailing partial sums, and every row that ends inside the step
@@ -65,12 +66,15 @@ constexpr int kThreads = 256;
 constexpr int kPer = 4;                 // positions per lane per step
 constexpr int kStep = 64 * kPer;        // positions per wave step
 constexpr int kWin = 512;               // row starts staged per LDS window (per wave)
-// Rows + nonzeros per wave (D == 1).  Halving the forward's range (more
-// waves, more gathers in flight per CU) took the forward from 150 to 142 us
-// and the dvals + dX backward from 269 to 260 us; the walks that gather
-// nothing (dX only, and dvals from the forward's gathered copy) are best
-// with the longer range (143 against 147 us; 65 against 72 us).
-constexpr int64_t kWaveItemsShort = 2048;
+// Rows + nonzeros per wave (D == 1).  A walk that gathers x runs as one
+// round of resident waves (gather_walk_waves), with at least kWaveItemsMin
+// items each.  At 2^20 rows and 16 M nonzeros (6 waves per SIMD fit) the
+// forward took 151 us with 4096 items per wave (0.7 of a round), 143 with
+// 2048 (1.4 rounds: a second, part-filled round), 141 with 1456 (2 rounds)
+// and 134 with 2902 (one full round).  The walks that gather nothing (dX
+// by atomics only, and dvals from the forward's gathered copy) keep the
+// longer fixed range (143 against 147 us; 65 against 72 us).
+constexpr int64_t kWaveItemsMin = 1024;
 constexpr int64_t kWaveItemsLong = 4096;
 
 template <typename I>
@@ -275,6 +279,13 @@ __device__ __forceinline__ void window_rows(const int64_t* bnd, const Walk& s, i
 
 // ------------------------------------------------------------ D == 1 forward
 // SAVE: also write xg[p] = x[col[p]] (column clamped) for every position.
+// Steps are aligned to multiples of kStep positions (a wave's first step
+// masks the positions before its first row), so position p always sits in
+// lane (p mod kStep) / 4, and a step cut short by the LDS window ends at a
+// row start.  With the positions past a cut keyed as a later row (below),
+// every row is summed in the same order however the rows are split between
+// waves: results do not depend on the wave count, which follows the
+// device's CU count and each instantiation's occupancy.
 template <typename I, bool VEC, bool SAVE>
 __device__ __forceinline__ void fwd_walk(const I* __restrict__ ptr, const I* __restrict__ col,
                                          const float* __restrict__ vals,
@@ -284,10 +295,10 @@ __device__ __forceinline__ void fwd_walk(const I* __restrict__ ptr, const I* __r
   float carry_val = 0.f;
   stage_window(ptr, nnz, s, lane, bnd);
   Quad<I, VEC> cur;
-  if (s.pos < s.b) cur.issue(col, vals, (s.pos & ~(int64_t)3) + kPer * lane, nnz);
+  if (s.pos < s.b) cur.issue(col, vals, (s.pos & ~(int64_t)(kStep - 1)) + kPer * lane, nnz);
 
   while (s.pos < s.b) {
-    const int64_t base = s.pos & ~(int64_t)3;
+    const int64_t base = s.pos & ~(int64_t)(kStep - 1);
     const int64_t want = min(base + kStep, s.b);
     if (s.wlimit < want && s.wr != s.carry_row) stage_window(ptr, nnz, s, lane, bnd);
     if (s.wlimit <= s.pos) {
@@ -308,7 +319,7 @@ __device__ __forceinline__ void fwd_walk(const I* __restrict__ ptr, const I* __r
 #pragma unroll
     for (int j = 0; j < 4; ++j) xv[j] = x[c[j]];
     Quad<I, VEC> nxt;  // the next step starts at step_end
-    nxt.issue(col, vals, (step_end & ~(int64_t)3) + kPer * lane, nnz);
+    nxt.issue(col, vals, (step_end & ~(int64_t)(kStep - 1)) + kPer * lane, nnz);
     if constexpr (SAVE) {
       // Streaming stores: the copy is read once, by the backward, and must
       // not displace x from L2.
@@ -323,6 +334,15 @@ __device__ __forceinline__ void fwd_walk(const I* __restrict__ ptr, const I* __r
     }
     int64_t rid[4];
     window_rows(bnd, s, q0, step_end - 1, rid);
+    // Positions at or past step_end (a step cut short by the window or by
+    // the wave's end) take a row id past the last real row: the rows in
+    // between are empty, and the last real row ends where it ends, as when
+    // another row follows it.  (Giving them the last real row instead would
+    // read that row's sum from lane 63, in another order of additions.)
+    const int64_t after = min(s.r1, s.wr + kWin);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (q0 + j >= step_end) rid[j] = after;
     float pr[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) pr[j] = in[j] ? v[j] * xv[j] : 0.f;
@@ -385,7 +405,8 @@ __device__ __forceinline__ void fwd_walk(const I* __restrict__ ptr, const I* __r
     s.pos = step_end;
     cur = nxt;
   }
-  if (lane == 0) y[s.carry_row] = carry_val;
+  // carry_row is r1 when the last step ended with positions past the end
+  if (lane == 0 && s.carry_row < s.r1) y[s.carry_row] = carry_val;
   for (int64_t r = s.carry_row + 1 + lane; r < s.r1; r += 64) y[r] = 0.f;
 }
 
@@ -1449,6 +1470,19 @@ int lanes_for(int64_t D, bool vec) {
   return units <= 4 ? 4 : (units <= 16 ? 16 : 64);
 }
 
+// Waves of a D == 1 walk kernel that gathers x (`items` = rows +
+// nonzeros): one round of the waves the device holds at once, so every wave
+// starts together and no part-filled round trails, but no more than one
+// wave per kWaveItemsMin items.
+int gather_walk_waves(const void* kernel, int64_t items, int64_t* n_waves) {
+  int resident = 1;
+  const int st = nl2k::resident_blocks(kernel, kThreads, &resident);
+  if (st) return st;
+  const int64_t waves = (int64_t)resident * (kThreads / 64);
+  *n_waves = std::max<int64_t>(1, std::min(waves, nl2k::ceil_div(items, kWaveItemsMin)));
+  return NL2K_SUCCESS;
+}
+
 // Xg != nullptr (D == 1 only): also write Xg[p] = X[col[p]] for the
 // backward's dvals.
 template <typename I>
@@ -1466,20 +1500,18 @@ int forward(const I* ptr, const I* col, const float* vals, const float* X, float
   if (!ptr || !X || !Y || (nnz > 0 && (!col || !vals)))
     return nl2k::fail(NL2K_ERR_NULL, "%s: null pointer argument", who);
   if (D == 1) {
-    const int64_t n_waves = std::max<int64_t>(1, nl2k::ceil_div(nnz + M, kWaveItemsShort));
-    const int64_t blocks = nl2k::ceil_div(n_waves, kThreads / 64);
-    if (blocks > INT32_MAX) return nl2k::fail(NL2K_ERR_OVERFLOW, "%s: too many rows", who);
     const bool save = want_xg && nnz > 0;
     const bool vec = nl2k::aligned16(col) && nl2k::aligned16(vals) && (!save || nl2k::aligned16(Xg));
-#define D1_FWD(V, SV)                                                                       \
-  hipLaunchKernelGGL((spmv_d1_fwd_kernel<I, V, SV>), dim3((unsigned)blocks), dim3(kThreads), 0, \
-                     stream, ptr, col, vals, X, Y, Xg, M, K, nnz, n_waves)
-    if (vec) {
-      if (save) D1_FWD(true, true); else D1_FWD(true, false);
-    } else {
-      if (save) D1_FWD(false, true); else D1_FWD(false, false);
-    }
-#undef D1_FWD
+    auto* kernel = vec ? (save ? &spmv_d1_fwd_kernel<I, true, true> : &spmv_d1_fwd_kernel<I, true, false>)
+                       : (save ? &spmv_d1_fwd_kernel<I, false, true>
+                               : &spmv_d1_fwd_kernel<I, false, false>);
+    int64_t n_waves = 1;
+    st = gather_walk_waves(reinterpret_cast<const void*>(kernel), nnz + M, &n_waves);
+    if (st) return st;
+    const int64_t blocks = nl2k::ceil_div(n_waves, kThreads / 64);
+    if (blocks > INT32_MAX) return nl2k::fail(NL2K_ERR_OVERFLOW, "%s: too many rows", who);
+    hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, ptr, col, vals,
+                       X, Y, Xg, M, K, nnz, n_waves);
     return nl2k::check_launch(who);
   }
   const bool vec = D % 4 == 0 && nl2k::aligned16(X) && nl2k::aligned16(Y);
@@ -1501,30 +1533,34 @@ int forward(const I* ptr, const I* col, const float* vals, const float* X, float
   return nl2k::check_launch(who);
 }
 
-// Xg != nullptr (dvals requested, mode kNoDx): the gathered walk.
+// Xg != nullptr (dvals requested, mode kNoDx): the gathered walk.  The
+// walks that gather x (dvals without Xg) run as one resident round; the
+// others take kWaveItemsLong items per wave.
 template <typename I>
-void launch_d1_bwd(bool vec, bool dv, int mode, unsigned blocks, hipStream_t stream,
-                   const I* ptr, const I* col, const float* vals, const float* X,
-                   const float* Xg, const float* dY, float* dvals, float* out, int64_t M,
-                   int64_t K, int64_t nnz, int64_t n_waves) {
-#define D1_BWD(V, DVV, MM, GG)                                                                   \
-  hipLaunchKernelGGL((spmv_d1_bwd_kernel<I, V, DVV, MM, GG>), dim3(blocks), dim3(kThreads), 0, \
-                     stream, ptr, col, vals, X, Xg, dY, dvals, out, M, K, nnz, n_waves)
-#define D1_BWD_MODE(V, DVV)                              \
-  if (mode == kAtomic) D1_BWD(V, DVV, kAtomic, false); \
-  else D1_BWD(V, DVV, kNoDx, false)
-  if (dv && Xg != nullptr && mode == kNoDx) {
-    if (vec) D1_BWD(true, true, kNoDx, true);
-    else D1_BWD(false, true, kNoDx, true);
-    return;
+int launch_d1_bwd(bool vec, bool dv, int mode, hipStream_t stream, const I* ptr, const I* col,
+                  const float* vals, const float* X, const float* Xg, const float* dY,
+                  float* dvals, float* out, int64_t M, int64_t K, int64_t nnz, const char* who) {
+  auto pick = [&](auto v) {
+    constexpr bool V = decltype(v)::value;
+    if (dv && Xg != nullptr && mode == kNoDx) return &spmv_d1_bwd_kernel<I, V, true, kNoDx, true>;
+    if (dv)
+      return mode == kAtomic ? &spmv_d1_bwd_kernel<I, V, true, kAtomic, false>
+                             : &spmv_d1_bwd_kernel<I, V, true, kNoDx, false>;
+    return mode == kAtomic ? &spmv_d1_bwd_kernel<I, V, false, kAtomic, false>
+                           : &spmv_d1_bwd_kernel<I, V, false, kNoDx, false>;
+  };
+  auto* kernel = vec ? pick(std::true_type{}) : pick(std::false_type{});
+  const bool gathers = dv && !(Xg != nullptr && mode == kNoDx);
+  int64_t n_waves = std::max<int64_t>(1, nl2k::ceil_div(nnz + M, kWaveItemsLong));
+  if (gathers) {
+    const int st = gather_walk_waves(reinterpret_cast<const void*>(kernel), nnz + M, &n_waves);
+    if (st) return st;
   }
-  if (vec) {
-    if (dv) { D1_BWD_MODE(true, true); } else { D1_BWD_MODE(true, false); }
-  } else {
-    if (dv) { D1_BWD_MODE(false, true); } else { D1_BWD_MODE(false, false); }
-  }
-#undef D1_BWD_MODE
-#undef D1_BWD
+  const int64_t blocks = nl2k::ceil_div(n_waves, kThreads / 64);
+  if (blocks > INT32_MAX) return nl2k::fail(NL2K_ERR_OVERFLOW, "%s: too many rows", who);
+  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, ptr, col, vals, X,
+                     Xg, dY, dvals, out, M, K, nnz, n_waves);
+  return nl2k::check_launch(who);
 }
 
 // dX by bucket sort (D == 1): bucket width `cols` = 2^shift, nb buckets,
@@ -1712,10 +1748,6 @@ int backward(const I* ptr, const I* col, const float* vals, const float* X, cons
     if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
       return nl2k::fail(NL2K_ERR_ALIGN, "%s: workspace must be 256-byte aligned", who);
   }
-  // the walk gathers x for dvals unless it reads the gathered copy (the
-  // atomic dX route, beyond the bucket limits, always gathers)
-  const bool gathers = dvals && !(Xg && !dX);
-  const int64_t wave_items = gathers ? kWaveItemsShort : kWaveItemsLong;
   if (sorted_dx) {
     // one kernel per sort tile forms the contributions (and dvals) and
     // sorts them by column bucket; one per bucket sums them into dx
@@ -1770,15 +1802,11 @@ int backward(const I* ptr, const I* col, const float* vals, const float* X, cons
   }
   if (M == 0 || nnz == 0 || (!dX && !dvals)) return nl2k::succeed();
   if (D == 1) {
-    const int64_t n_waves = std::max<int64_t>(1, nl2k::ceil_div(nnz + M, wave_items));
-    const int64_t blocks = nl2k::ceil_div(n_waves, kThreads / 64);
-    if (blocks > INT32_MAX) return nl2k::fail(NL2K_ERR_OVERFLOW, "%s: too many rows", who);
     const bool vec = nl2k::aligned16(col) && nl2k::aligned16(vals) &&
                      (dvals == nullptr || nl2k::aligned16(dvals)) &&
                      (Xg == nullptr || nl2k::aligned16(Xg));
-    launch_d1_bwd<I>(vec, dvals != nullptr, dX ? kAtomic : kNoDx, (unsigned)blocks, stream, ptr,
-                     col, vals, X, Xg, dY, dvals, dX, M, K, nnz, n_waves);
-    return nl2k::check_launch(who);
+    return launch_d1_bwd<I>(vec, dvals != nullptr, dX ? kAtomic : kNoDx, stream, ptr, col, vals,
+                            X, Xg, dY, dvals, dX, M, K, nnz, who);
   }
   const bool vec = D % 4 == 0 && nl2k::aligned16(X) && nl2k::aligned16(dY) &&
                    (dX == nullptr || nl2k::aligned16(dX));

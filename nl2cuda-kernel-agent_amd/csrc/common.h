@@ -9,10 +9,14 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstddef>
 #include <cstdint>
 #include <cstdio>
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "nl2k_status.h"
 
@@ -61,6 +65,39 @@ inline int check_hip(hipError_t e, const char* what) {
 }
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Workgroups of `kernel` (launched with `threads` threads and no dynamic LDS)
+// that the current device holds at once: its CU count times the occupancy
+// the runtime computes from the kernel's registers, LDS and launch bounds.
+// Cached per (device, kernel), so instantiations with equal signatures but
+// different register counts keep their own figures.
+inline int resident_blocks(const void* kernel, int threads, int* out) {
+  static std::mutex mu;
+  static std::map<std::pair<int, const void*>, int> cache;
+  int dev = 0;
+  int st = check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (st) return st;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    const auto it = cache.find({dev, kernel});
+    if (it != cache.end()) {
+      *out = it->second;
+      return NL2K_SUCCESS;
+    }
+  }
+  int cus = 0, per_cu = 0;
+  st = check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev),
+                 "hipDeviceGetAttribute(MultiprocessorCount)");
+  if (st) return st;
+  st = check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0),
+                 "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+  if (st) return st;
+  const int n = std::max(1, cus) * std::max(1, per_cu);
+  std::lock_guard<std::mutex> lock(mu);
+  cache[{dev, kernel}] = n;
+  *out = n;
+  return NL2K_SUCCESS;
+}
 
 // -------------------------------------------------------------- device side
 typedef float f32x4 __attribute__((ext_vector_type(4)));

@@ -4,7 +4,8 @@ int32 and int64 indices, D = 1, forward and backward), the reference's
 default case through verify_all, structures with empty rows, runs of empty
 rows longer than the staged window, long rows, K = 1, nnz = 0, feature
 widths across every SpMM lane class, misaligned value arrays, determinism
-and the adjoint identities."""
+(also under a different split of the rows between waves) and the adjoint
+identities."""
 
 import numpy as np
 import pytest
@@ -126,6 +127,27 @@ def test_spmv_zipf_int64_matches_int32(zipf_inputs):
     lhs = float((y64.double() * dY.double()).sum())
     assert np.isclose(lhs, float((args32[3].double() * dX64.double()).sum()), rtol=1e-4)
     assert np.isclose(lhs, float((args32[2].double() * dv64.double()).sum()), rtol=1e-4)
+
+
+@pytest.mark.parametrize("pad", [(777, 0), (0, 1234), (5, 300_001)])
+def test_spmv_d1_forward_independent_of_wave_split(zipf_inputs, pad):
+    """Empty rows before and after the matrix move every boundary of the
+    merge-path split between waves (and the wave count) but no nonzero: the
+    real rows must come out bit-identical and the padding rows 0."""
+    announce(f"spmv zipf 2^20 forward with {pad} empty rows around it")
+    from cases.spmv import op
+    t = zipf_inputs
+    ptr, col, vals, X = (t[k].cuda() for k in ("row_ptr", "col_idx", "vals", "X"))
+    before, after = pad
+    nnz = int(ptr[-1])
+    ptr_p = torch.cat([torch.zeros(before, dtype=ptr.dtype, device=ptr.device), ptr,
+                       torch.full((after,), nnz, dtype=ptr.dtype, device=ptr.device)])
+    y = op.spmv_forward(ptr, col, vals, X)
+    y_p = op.spmv_forward(ptr_p, col, vals, X)
+    torch.cuda.synchronize()
+    M = ptr.numel() - 1
+    assert torch.equal(y_p[before:before + M], y)
+    assert not torch.any(y_p[:before]) and not torch.any(y_p[before + M:])
 
 
 @pytest.mark.parametrize("idx", [torch.int64, torch.int32])
