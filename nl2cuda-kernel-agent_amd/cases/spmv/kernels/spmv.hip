@@ -12,8 +12,9 @@
 //    merge-path coordinate f(r) = row_ptr[r] + r, so every wave gets about S
 //    rows-plus-nonzeros and owns its rows outright (no cross-wave carries,
 //    no atomics, deterministic); S is chosen so that the launch is one round
-//    of the waves the device holds at once.  A wave finds its first row with a
-//    64-way parallel search (four dependent probes at M = 2^20), then walks
+//    of the waves the device holds at once.  Rows are found with a 64-way
+//    parallel search (four dependent probes at M = 2^20) of the workgroup's
+//    range, then a short one per wave inside it.  A wave then walks
 //    its nonzeros in steps of 256: lane l loads positions 4l..4l+3 with one
 //    16-byte load of col_idx and one of vals, gathers x, and finds each
 //    position's row by binary search over the next 512 row starts staged in
@@ -91,12 +92,13 @@ __device__ __forceinline__ int64_t ld_col(const I* __restrict__ col, int64_t p, 
 
 __device__ __forceinline__ int lane_count(bool pred) { return __popcll(__ballot(pred)); }
 
-// First r in [0, M] with row_ptr[r] + wr * r >= target (wave-uniform
-// result): wr = 1 searches the merge-path coordinate, wr = 0 row starts.
+// First r in [lo, hi] with row_ptr[r] + wr * r >= target, given that the
+// answer lies in that range (wave-uniform result): wr = 1 searches the
+// merge-path coordinate, wr = 0 row starts.
 template <typename I>
-__device__ int64_t rows_lower_bound(const I* __restrict__ ptr, int64_t M, int64_t nnz,
-                                    int64_t target, int lane, int64_t wr = 1) {
-  int64_t lo = 0, hi = M;
+__device__ int64_t rows_lower_bound_in(const I* __restrict__ ptr, int64_t lo, int64_t hi,
+                                       int64_t nnz, int64_t target, int lane, int64_t wr = 1) {
+  const int64_t top = hi;
   while (hi - lo > 63) {
     const int64_t step = (hi - lo + 63) / 64;
     const int64_t probe = min(hi, lo + (int64_t)lane * step);
@@ -108,7 +110,14 @@ __device__ int64_t rows_lower_bound(const I* __restrict__ ptr, int64_t M, int64_
   }
   const int64_t probe = min(hi, lo + lane);
   const int c = lane_count(lo + lane <= hi && ld_ptr(ptr, probe, nnz) + wr * probe < target);
-  return min(lo + c, M);
+  return min(lo + c, top);
+}
+
+// First r in [0, M] with row_ptr[r] + wr * r >= target.
+template <typename I>
+__device__ int64_t rows_lower_bound(const I* __restrict__ ptr, int64_t M, int64_t nnz,
+                                    int64_t target, int lane, int64_t wr = 1) {
+  return rows_lower_bound_in(ptr, 0, M, nnz, target, lane, wr);
 }
 
 // The raw col_idx / vals entries of positions q0..q0+3 (q0 % 4 == 0),
@@ -221,12 +230,40 @@ struct Walk {
   int64_t wlimit;       // start of row wr + kWin: positions below it resolve
 };
 
+// Row ranges of a workgroup's four waves: wave w owns the rows from the
+// first r with row_ptr[r] + r >= w * per up to the next wave's first row.
+// Wave 0 finds the workgroup's first row and wave 1 the row past its last
+// one, searching all M rows; waves 1-3 then find their own first rows
+// inside that range (a short search), so a workgroup makes two full
+// searches instead of eight.  Every wave of the workgroup calls this (it
+// holds two barriers); it returns whether the wave has work.
 template <typename I>
 __device__ __forceinline__ bool walk_begin(const I* __restrict__ ptr, int64_t M, int64_t nnz,
-                                           int64_t w, int64_t n_waves, int lane, Walk& s) {
+                                           int64_t n_waves, int lane, int wave,
+                                           int64_t* starts, Walk& s) {
   const int64_t per = (nnz + M + n_waves - 1) / n_waves;  // items per wave
-  s.r0 = w == 0 ? 0 : rows_lower_bound(ptr, M, nnz, w * per, lane);
-  s.r1 = w == n_waves - 1 ? M : rows_lower_bound(ptr, M, nnz, (w + 1) * per, lane);
+  const int64_t w0 = (int64_t)blockIdx.x * (kThreads / 64);  // < n_waves
+  // starts[q] = first row of wave w0 + q (M for waves past the last)
+  if (wave == 0) {
+    const int64_t r = w0 == 0 ? 0 : rows_lower_bound(ptr, M, nnz, w0 * per, lane);
+    if (lane == 0) starts[0] = r;
+  } else if (wave == 1) {
+    const int64_t wn = w0 + kThreads / 64;
+    const int64_t r = wn >= n_waves ? M : rows_lower_bound(ptr, M, nnz, wn * per, lane);
+    if (lane == 0) starts[kThreads / 64] = r;
+  }
+  __syncthreads();
+  const int64_t w = w0 + wave;
+  if (wave > 0) {
+    const int64_t r = w >= n_waves ? M
+                                   : rows_lower_bound_in(ptr, starts[0], starts[kThreads / 64], nnz,
+                                                         w * per, lane);
+    if (lane == 0) starts[wave] = r;
+  }
+  __syncthreads();
+  if (w >= n_waves) return false;
+  s.r0 = starts[wave];
+  s.r1 = starts[wave + 1];
   if (s.r1 <= s.r0) return false;
   s.pos = ld_ptr(ptr, s.r0, nnz);
   s.b = max(s.pos, ld_ptr(ptr, s.r1, nnz));
@@ -416,12 +453,11 @@ __global__ __launch_bounds__(kThreads) void spmv_d1_fwd_kernel(
     const float* __restrict__ x, float* __restrict__ y, float* __restrict__ xg, int64_t M,
     int64_t K, int64_t nnz, int64_t n_waves) {
   __shared__ int64_t bnd_s[kThreads / 64][kWin];
+  __shared__ int64_t starts[kThreads / 64 + 1];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int64_t w = (int64_t)blockIdx.x * (kThreads / 64) + wave;
-  if (w >= n_waves) return;  // wave-uniform; the kernel has no workgroup barrier
   Walk s;
-  if (!walk_begin(ptr, M, nnz, w, n_waves, lane, s)) return;
+  if (!walk_begin(ptr, M, nnz, n_waves, lane, wave, starts, s)) return;  // wave-uniform
   if constexpr (VEC) {
     if (s.b <= (nnz & ~(int64_t)3)) {
       fwd_walk<I, true, SAVE>(ptr, col, vals, x, y, xg, K, nnz, s, lane, bnd_s[wave]);
@@ -525,12 +561,11 @@ __global__ __launch_bounds__(kThreads) void spmv_d1_bwd_kernel(
     float* __restrict__ dvals, float* __restrict__ out, int64_t M, int64_t K, int64_t nnz,
     int64_t n_waves) {
   __shared__ int64_t bnd_s[kThreads / 64][kWin];
+  __shared__ int64_t starts[kThreads / 64 + 1];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int64_t w = (int64_t)blockIdx.x * (kThreads / 64) + wave;
-  if (w >= n_waves) return;
   Walk s;
-  if (!walk_begin(ptr, M, nnz, w, n_waves, lane, s)) return;
+  if (!walk_begin(ptr, M, nnz, n_waves, lane, wave, starts, s)) return;
   if (s.pos >= s.b) return;
   if constexpr (VEC) {
     if (s.b <= (nnz & ~(int64_t)3)) {
