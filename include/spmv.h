@@ -13,7 +13,9 @@
  * 0 <= col_idx < K) cannot be checked without reading device memory; the
  * kernels clamp every index they load into range, so a malformed structure
  * gives wrong numbers, never an out-of-bounds access.  The forward and
- * dvals are deterministic.  At D > 1 with K <= 16384 (the reference's
+ * dvals are deterministic; the D == 1 forward's order of additions does not
+ * depend on how rows are split between waves (which follows the device's CU
+ * count), so it gives the same bits on any device.  At D > 1 with K <= 16384 (the reference's
  * default SpMM: M = K = 4096, D = 64) dX is deterministic too: a stable
  * column-major copy of A is built in the workspace and each dX row is
  * summed over its column's entries in position order.  At D == 1, and at
