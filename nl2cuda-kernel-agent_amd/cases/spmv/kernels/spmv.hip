@@ -127,6 +127,9 @@ __device__ int64_t rows_lower_bound(const I* __restrict__ ptr, int64_t M, int64_
 // nnz_full = nnz rounded down to a multiple of 4; a wave takes it only when
 // all its positions lie below nnz_full, so no entry it uses is clamped.  The
 // scalar form reads each entry at its position clamped to [0, nnz - 1].
+// The vector loads are nontemporal: the structure is read once, and lines
+// that do not stay in the L2 leave more of it to the gathered x (forward
+// 131.0 -> 127.7 us at the acceptance shape).
 template <typename I, bool VEC>
 struct Quad {
   I c[4];
@@ -150,8 +153,8 @@ struct Quad<int32_t, true> {
   __device__ void issue(const int32_t* __restrict__ col, const float* __restrict__ vals,
                         int64_t q0, int64_t nnz) {
     const int64_t q = max((int64_t)0, min(q0, (nnz & ~(int64_t)3) - 4));
-    c = *reinterpret_cast<const i32x4_t*>(col + q);
-    v = *reinterpret_cast<const f32x4*>(vals + q);
+    c = __builtin_nontemporal_load(reinterpret_cast<const i32x4_t*>(col + q));
+    v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(vals + q));
   }
   __device__ int64_t col_at(int j) const { return (int64_t)c[j]; }
   __device__ float val_at(int j) const { return v[j]; }
@@ -163,9 +166,9 @@ struct Quad<int64_t, true> {
   __device__ void issue(const int64_t* __restrict__ col, const float* __restrict__ vals,
                         int64_t q0, int64_t nnz) {
     const int64_t q = max((int64_t)0, min(q0, (nnz & ~(int64_t)3) - 4));
-    c0 = *reinterpret_cast<const i64x2_t*>(col + q);
-    c1 = *reinterpret_cast<const i64x2_t*>(col + q + 2);
-    v = *reinterpret_cast<const f32x4*>(vals + q);
+    c0 = __builtin_nontemporal_load(reinterpret_cast<const i64x2_t*>(col + q));
+    c1 = __builtin_nontemporal_load(reinterpret_cast<const i64x2_t*>(col + q + 2));
+    v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(vals + q));
   }
   __device__ int64_t col_at(int j) const { return j < 2 ? c0[j] : c1[j - 2]; }
   __device__ float val_at(int j) const { return v[j]; }
@@ -1247,6 +1250,18 @@ __device__ __forceinline__ T* at_byte(T* base, unsigned off) {
   return reinterpret_cast<T*>(reinterpret_cast<C*>(base) + off);
 }
 
+// Loads and stores with the nontemporal hint when NT (same values).
+template <bool NT, typename T>
+__device__ __forceinline__ T ld_hint(const T* p) {
+  if constexpr (NT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+template <bool NT, typename T>
+__device__ __forceinline__ void st_hint(T v, T* p) {
+  if constexpr (NT) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
+
 // Sort tile t = positions [kSortTile t, kSortTile (t + 1)): each position's
 // contribution vals[p] * dy[row(p)] -- and dvals[p] = dy[row(p)] *
 // x[col(p)], from the forward's gathered copy of x (kDvKept) or by
@@ -1273,6 +1288,13 @@ __global__ __launch_bounds__(kSortThreads) void spmv_walk_sort_kernel(
   __shared__ uint16_t s_low[kSortTile];
   __shared__ unsigned s_cur[kMaxBuckets];
   __shared__ unsigned s_wave[kSortThreads / 64];
+  // Nontemporal hints where they measured faster at the acceptance shape
+  // (Zipf 2^20, int32): structure loads when dvals are formed (gathering
+  // 183.2 -> 180.8 us, kept x 126.8 -> 125.9; dX alone 103.5 -> 104.5
+  // with them), output stores when x is gathered (180.8 -> 177.5 us; the
+  // other variants slower by 1.5-2.5 us), where they keep the L2 for x.
+  constexpr bool kNtLoads = DVM != kDvNone;
+  constexpr bool kNtStores = DVM == kDvGather;
   // row_ptr[ra + 1 + k] - lo, clamped into [0, kSortTile]: read before the
   // first barrier of the counting step, s_val written after it
   int* s_win = reinterpret_cast<int*>(s_val);
@@ -1302,16 +1324,18 @@ __global__ __launch_bounds__(kSortThreads) void spmv_walk_sort_kernel(
 #pragma unroll
     for (int g = 0; g < kSortPer / 4; ++g) {
       const unsigned i = min(4u * (unsigned)(tid + kSortThreads * g), (unsigned)n - 4u);
-      const f32x4 v4 = *reinterpret_cast<const f32x4*>(at_byte(vt, 4u * i));
+      const f32x4 v4 = ld_hint<kNtLoads>(reinterpret_cast<const f32x4*>(at_byte(vt, 4u * i)));
       f32x4 x4 = f32x4{0.f, 0.f, 0.f, 0.f};
-      if constexpr (DVM == kDvKept) x4 = *reinterpret_cast<const f32x4*>(at_byte(xt, 4u * i));
+      if constexpr (DVM == kDvKept)
+        x4 = ld_hint<kNtLoads>(reinterpret_cast<const f32x4*>(at_byte(xt, 4u * i)));
       if constexpr (sizeof(I) == 4) {
-        const i32x4_t ci = *reinterpret_cast<const i32x4_t*>(at_byte(ct, 4u * i));
+        const i32x4_t ci = ld_hint<kNtLoads>(reinterpret_cast<const i32x4_t*>(at_byte(ct, 4u * i)));
 #pragma unroll
         for (int j = 0; j < 4; ++j) craw[4 * g + j] = ci[j];
       } else {
-        const i64x2_t c0 = *reinterpret_cast<const i64x2_t*>(at_byte(ct, 8u * i));
-        const i64x2_t c1 = *reinterpret_cast<const i64x2_t*>(at_byte(ct, 8u * i + 16u));
+        const i64x2_t c0 = ld_hint<kNtLoads>(reinterpret_cast<const i64x2_t*>(at_byte(ct, 8u * i)));
+        const i64x2_t c1 =
+            ld_hint<kNtLoads>(reinterpret_cast<const i64x2_t*>(at_byte(ct, 8u * i + 16u)));
         craw[4 * g + 0] = c0[0];
         craw[4 * g + 1] = c0[1];
         craw[4 * g + 2] = c1[0];
@@ -1469,8 +1493,10 @@ __global__ __launch_bounds__(kSortThreads) void spmv_walk_sort_kernel(
   uint16_t* __restrict__ lw = lowcol + lo;
   for (int i = 4 * tid; i < n; i += 4 * kSortThreads) {
     if (i + 3 < n) {
-      *reinterpret_cast<f32x4*>(at_byte(vo, 4u * i)) = *reinterpret_cast<const f32x4*>(s_val + i);
-      *reinterpret_cast<uint2*>(at_byte(lw, 2u * i)) = *reinterpret_cast<const uint2*>(s_low + i);
+      st_hint<kNtStores>(*reinterpret_cast<const f32x4*>(s_val + i),
+                         reinterpret_cast<f32x4*>(at_byte(vo, 4u * i)));
+      st_hint<kNtStores>(*reinterpret_cast<const uint64_t*>(s_low + i),
+                         reinterpret_cast<uint64_t*>(at_byte(lw, 2u * i)));
     } else {
       for (int j = i; j < n; ++j) {
         *at_byte(vo, 4u * j) = s_val[j];
