@@ -535,8 +535,10 @@ __device__ __forceinline__ void bwd_walk(const I* __restrict__ ptr, const I* __r
     const bool full = in[0] && in[3];
     if constexpr (DV) {
       if (VEC && full) {
-        *reinterpret_cast<f32x4*>(dvals + q0) =
-            f32x4{g[0] * xv[0], g[1] * xv[1], g[2] * xv[2], g[3] * xv[3]};
+        // nontemporal, like the sort kernel's dvals stores (dvals-only
+        // walk 132.3 -> 129.8 us): dvals is not read again here
+        __builtin_nontemporal_store(f32x4{g[0] * xv[0], g[1] * xv[1], g[2] * xv[2], g[3] * xv[3]},
+                                    reinterpret_cast<f32x4*>(dvals + q0));
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -1435,7 +1437,8 @@ __global__ __launch_bounds__(kSortThreads) void spmv_walk_sort_kernel(
     }
     if constexpr (DVM != kDvNone) {
       if (VEC && in[0] && in[1] && in[2] && in[3]) {
-        *reinterpret_cast<f32x4*>(at_byte(dvt, 4u * i0)) = dv;
+        // nontemporal: gathering 178.9 -> 174.3 us, kept x 126.2 -> 123.5
+        __builtin_nontemporal_store(dv, reinterpret_cast<f32x4*>(at_byte(dvt, 4u * i0)));
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
