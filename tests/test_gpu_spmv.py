@@ -203,6 +203,15 @@ def _lens(kind, m, k, rng):
         return np.minimum(rng.zipf(1.5, m), k)
     if kind == "sparse_rows":  # rows of 0-1 nonzeros: sort tiles span more rows than their LDS copy
         return (rng.random(m) < 0.15).astype(np.int64)
+    if kind == "ragged_long":  # SpMM rows split between lane groups: long, empty and 1-entry rows
+        lens = rng.integers(0, 300, m)
+        lens[::7] = 0
+        lens[1::11] = 1
+        return lens
+    if kind == "long":
+        return rng.integers(100, 400, m)
+    if kind == "mid":
+        return rng.integers(0, 48, m)
     if kind == "tile_edges":  # rows starting on 8192-position sort-tile edges, empty ones too
         lens = np.full(m, 8, np.int64)
         lens[1024] = 0  # rows 1024 and 1025 both start at position 8192
@@ -219,7 +228,10 @@ def _lens(kind, m, k, rng):
     ("zipf", 300, 200, 17), ("zipf", 300, 200, 64), ("small", 100, 100, 100),
     ("small", 100, 50, 256), ("one_long", 64, 64, 300), ("ends_only", 700, 90, 8),
     ("small", 300, 20000, 4), ("small", 300, 16384, 8), ("mostly_empty", 2000, 1500, 32), ("one_long", 50, 3000, 16),
-    ("sparse_rows", 200000, 5000, 1), ("tile_edges", 6000, 3000, 1)])
+    ("sparse_rows", 200000, 5000, 1), ("tile_edges", 6000, 3000, 1),
+    ("ragged_long", 333, 500, 3), ("ragged_long", 333, 500, 8), ("ragged_long", 333, 500, 20),
+    ("ragged_long", 333, 500, 64), ("ragged_long", 129, 700, 100), ("long", 77, 900, 8),
+    ("long", 77, 900, 5), ("mid", 1001, 300, 12), ("mid", 1001, 300, 64)])
 def test_spmv_structures(kind, m, k, d):
     announce(f"spmv {kind} M={m} K={k} D={d}")
     rng = np.random.default_rng(m + k + d)
