@@ -1,6 +1,7 @@
 """Graph capture of the launches that hand values between workgroups
 through nonce-tagged slots (the long-row scan, the softmax CE forward and
-the column offsets of the SpMM backward).
+the column offsets of the SpMM backward), and of the SpMV D = 1 forward and
+sorted backward.
 A captured launch keeps the nonce it was captured with, so the libraries
 clear the slots with a fill kernel captured ahead of it.  Each test replays
 one graph several times on new inputs, with eager calls and
@@ -117,3 +118,41 @@ def test_spmm_backward_graph_replays_with_new_inputs():
         edv, edx = op.spmv_backward(ptr, col, vals, X, dy_static.clone())
         torch.cuda.synchronize()
         assert torch.equal(edx, dx_static) and torch.equal(edv, dv_static), f"replay {seed}"
+
+
+def test_spmv_d1_graph_replays_with_new_inputs():
+    """The D = 1 forward (one resident round of walk waves) and the sorted dX
+    backward (row table, sort, bucket sums over a workspace with no initial
+    contents) captured once and replayed on new x and dy."""
+    announce("spmv D=1 forward + backward graph capture (Zipf 2^16)")
+    from cases.spmv import op, reference as ref
+    from oracle import spmv as osp
+    m = k = 1 << 16
+    t = ref.make_zipf_inputs(m, k, 1, 5, torch.int32)
+    ptr, col, vals = (t[n].cuda() for n in ("row_ptr", "col_idx", "vals"))
+    x_static = torch.zeros(k, 1, device="cuda")
+    dy_static = torch.zeros(m, 1, device="cuda")
+
+    def step():
+        y = op.spmv_forward(ptr, col, vals, x_static)
+        dv, dx = op.spmv_backward(ptr, col, vals, x_static, dy_static)
+        return y, dv, dx
+
+    g, (y_s, dv_s, dx_s) = _capture(step)
+    hp, hc, hv = (t[n].numpy() for n in ("row_ptr", "col_idx", "vals"))
+    for seed in range(3):
+        gen = torch.Generator().manual_seed(500 + seed)
+        x, dy = torch.randn(k, 1, generator=gen), torch.randn(m, 1, generator=gen)
+        x_static.copy_(x.cuda())
+        dy_static.copy_(dy.cuda())
+        g.replay()
+        torch.cuda.synchronize()
+        ry = osp.forward_f64(hp, hc, hv, x.numpy())
+        rdv, rdx = osp.backward_f64(hp, hc, hv, x.numpy(), dy.numpy())
+        for name, got, ref_ in (("y", y_s, ry), ("dvals", dv_s, rdv), ("dX", dx_s, rdx)):
+            err = np.abs(got.cpu().double().numpy() - ref_)
+            print(f"  replay {seed} {name}: max_abs={err.max():.3e}")
+            assert np.all(err <= 1e-3 + 1e-3 * np.abs(ref_)), f"replay {seed}: {name}"
+        ey, edv, _ = step()
+        torch.cuda.synchronize()
+        assert torch.equal(ey, y_s) and torch.equal(edv, dv_s), f"replay {seed}"
