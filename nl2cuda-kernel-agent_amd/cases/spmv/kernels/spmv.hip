@@ -1171,8 +1171,12 @@ __global__ __launch_bounds__(kThreads) void spmm_t_scatter_kernel(
 // and shuffle each entry's fields to the whole group, which then loads the
 // 16 dY rows together; the next step's records are loaded while those rows
 // are in flight.  Entries past the column's end repeat its last entry (valid
-// addresses) and are masked out of the sums and stores.
-template <typename I, int L, bool VEC, bool DV>
+// addresses) and are masked out of the sums and stores.  G groups of L lanes
+// share a column: group g takes its steps g, g + G, ... (16 entries each),
+// and the G partial sums are added by an xor butterfly, so more waves share
+// a long column's chain of record -> row loads.  Lanes of columns past K run
+// empty, since every lane takes part in the butterfly.
+template <typename I, int L, int G, bool VEC, bool DV>
 __global__ __launch_bounds__(kThreads) void spmm_t_gather_kernel(
     const I* __restrict__ colptr, const i32x4_t* __restrict__ crec,
     const float* __restrict__ X, const float* __restrict__ dY, float* __restrict__ dX,
@@ -1180,15 +1184,16 @@ __global__ __launch_bounds__(kThreads) void spmm_t_gather_kernel(
   using V = Lanes<VEC>;
   constexpr int E = 16;                   // entries per step
   constexpr int RPL = (E + L - 1) / L;    // records per lane per step
-  const int64_t c = (int64_t)blockIdx.x * (kThreads / L) + threadIdx.x / L;
+  constexpr int kColLanes = L * G;
+  static_assert(kColLanes <= 64 && (kColLanes & (kColLanes - 1)) == 0, "columns inside a wave");
+  const int64_t c = (int64_t)blockIdx.x * (kThreads / kColLanes) + threadIdx.x / kColLanes;
   const int gl = threadIdx.x % L;
+  const int grp = (threadIdx.x % kColLanes) / L;
   const int gbase = (threadIdx.x & 63) - gl;  // first lane of the group in the wave
-  if (c >= K) return;  // whole groups exit together (L divides 64)
-  const int64_t s = ld_ptr(colptr, c, nnz), e = max(s, ld_ptr(colptr, c + 1, nnz));
-  if (s == e) {
-    for (int64_t d = (int64_t)gl * V::W; d < D; d += (int64_t)L * V::W) V::store(dX + c * D + d, V::zero());
-    return;
-  }
+  const bool live = c < K;
+  const int64_t cc = live ? c : 0;
+  const int64_t s = live ? ld_ptr(colptr, c, nnz) : 0;
+  const int64_t e = live ? max(s, ld_ptr(colptr, c + 1, nnz)) : 0;
   auto load_recs = [&](int64_t q, i32x4_t (&r)[RPL]) {
 #pragma unroll
     for (int j = 0; j < RPL; ++j) r[j] = crec[max(s, min(q + gl + (int64_t)L * j, e - 1))];
@@ -1198,11 +1203,12 @@ __global__ __launch_bounds__(kThreads) void spmm_t_gather_kernel(
     const bool active = d < D;
     const int64_t dc = active ? d : 0;
     typename V::T xc = V::zero();
-    if (DV) xc = V::load(X + c * D + dc);
+    if (DV) xc = V::load(X + cc * D + dc);
     typename V::T acc = V::zero();
     i32x4_t rec[RPL];
-    load_recs(s, rec);
-    for (int64_t q = s; q < e; q += E) {
+    const int64_t q0 = s + (int64_t)grp * E;
+    if (q0 < e) load_recs(q0, rec);  // a column with no entries reads nothing
+    for (int64_t q = q0; q < e; q += (int64_t)G * E) {
       const int my_pos = rec[0][1];  // L == 16: lane gl holds entry gl's record
       int rr[E], pp[E];
       float vv[E];  // zero past the column's end, so the sum needs no branch
@@ -1220,7 +1226,7 @@ __global__ __launch_bounds__(kThreads) void spmm_t_gather_kernel(
         const int64_t r = min(max((int64_t)rr[u], (int64_t)0), M - 1);
         gs[u] = V::load(dY + r * D + dc);
       }
-      load_recs(q + E, rec);
+      load_recs(q + (int64_t)G * E, rec);
       // every row load is in flight before the first use (left alone, the
       // compiler sinks each load to its add and waits for it there)
       __builtin_amdgcn_sched_barrier(0);
@@ -1260,7 +1266,8 @@ __global__ __launch_bounds__(kThreads) void spmm_t_gather_kernel(
         }
       }
     }
-    if (active) V::store(dX + c * D + d, acc);
+    if constexpr (G > 1) acc = groups_sum<L, G>(acc);
+    if (live && active && grp == 0) V::store(dX + c * D + d, acc);
   }
 }
 
@@ -1572,6 +1579,16 @@ int lanes_for(int64_t D, bool vec) {
   return units <= 4 ? 4 : (units <= 16 ? 16 : 64);
 }
 
+// Groups of L lanes that share a column in the SpMM backward's gather: 2
+// when L * 2 <= 64 and an average column has two 16-entry steps or more,
+// else 1.  At the reference default (64 entries per column, L = 16, 159
+// VGPRs: 3 waves per SIMD) the backward measured 41.9 us with G = 1, 39.5
+// with G = 2 and 41.2 with G = 4, whose 4096 waves overflow one round.
+int spmm_col_groups(int L, int64_t K, int64_t nnz) {
+  const int64_t avg = K > 0 ? nnz / K : 0;
+  return (2 * L <= 64 && avg >= 32) ? 2 : 1;
+}
+
 // Groups of L lanes that split each row's nonzeros in the SpMM forward: the
 // largest power of two with L * G <= 64 that leaves each group about 8 or
 // more nonzeros of an average row (G = 4 at the reference default: 64 per
@@ -1810,21 +1827,26 @@ int transpose_backward(const TransposePlan& tp, const I* ptr, const I* col, cons
                    nl2k::aligned16(dX);
   const int L = lanes_for(D, vec);
   const bool dv = dvals != nullptr && D <= (int64_t)L * (vec ? 4 : 1);
-  const int64_t blocks = nl2k::ceil_div(K, kThreads / L);
+  const int G = spmm_col_groups(L, K, nnz);
+  const int64_t blocks = nl2k::ceil_div(K, kThreads / (L * G));
   const dim3 grid((unsigned)blocks), block(kThreads);
-#define SPMM_T(LL, VV, DVV)                                                                   \
-  hipLaunchKernelGGL((spmm_t_gather_kernel<I, LL, VV, DVV>), grid, block, 0, stream, colptr, \
+#define SPMM_T(LL, GG, VV, DVV)                                                                   \
+  hipLaunchKernelGGL((spmm_t_gather_kernel<I, LL, GG, VV, DVV>), grid, block, 0, stream, colptr, \
                      crec, X, dY, dX, dvals, M, K, D, nnz)
+#define SPMM_T_G(LL, VV, DVV)         \
+  if (G == 1) SPMM_T(LL, 1, VV, DVV); \
+  else SPMM_T(LL, 2, VV, DVV)
 #define SPMM_T_L(VV, DVV)                     \
-  if (L == 4) SPMM_T(4, VV, DVV);             \
-  else if (L == 16) SPMM_T(16, VV, DVV);      \
-  else SPMM_T(64, VV, DVV)
+  if (L == 4) { SPMM_T_G(4, VV, DVV); }       \
+  else if (L == 16) { SPMM_T_G(16, VV, DVV); } \
+  else SPMM_T(64, 1, VV, DVV)
   if (vec) {
     if (dv) { SPMM_T_L(true, true); } else { SPMM_T_L(true, false); }
   } else {
     if (dv) { SPMM_T_L(false, true); } else { SPMM_T_L(false, false); }
   }
 #undef SPMM_T_L
+#undef SPMM_T_G
 #undef SPMM_T
   st = nl2k::check_launch(who);
   if (st || dvals == nullptr || dv) return st;
