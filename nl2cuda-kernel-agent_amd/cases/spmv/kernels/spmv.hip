@@ -39,13 +39,15 @@
 //    column varies between runs, as with the reference's atomics.  Column
 //    counts too large for 1024 buckets of 16384 columns fall back to
 //    zero-fill plus fp32 atomics from the walk.
-//  * D > 1 (SpMM): L lanes per row (L = 4, 16 or 64), float4 columns when
-//    D % 4 == 0 and X / Y are 16-byte aligned; the lanes of a row share each
-//    (col, val) load and read the X row coalesced.  Backward (K <= 16384):
-//    dX = A^T dY through a stable column-major copy of A built in the
-//    workspace (chunk histograms, column offsets, an in-order scatter), then
-//    the same lane-group gather per column, with dvals from the same pass;
-//    deterministic, no atomics (the spmm_t_* kernels below).  Beyond 16384
+//  * D > 1 (SpMM): groups of L lanes cover a row's columns (L = 4, 16 or
+//    64), float4 columns when D % 4 == 0 and X / Y are 16-byte aligned; the
+//    lanes of a group share each (col, val) load and read the X row
+//    coalesced, and G groups split a long row's nonzeros (their sums added
+//    by an xor butterfly).  Backward (K <= 16384): dX = A^T dY through a
+//    stable column-major copy of A built in the workspace (chunk histograms,
+//    column offsets, an in-order scatter), then the same lane-group gather
+//    per column, with dvals from the same pass; deterministic, no atomics
+//    (the spmm_t_* kernels below).  Beyond 16384
 //    columns: per nonzero a group reduction for dvals and per-element
 //    atomics for dX.
 #include <algorithm>
