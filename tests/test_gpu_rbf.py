@@ -4,7 +4,7 @@ autograd op) against the float64 oracle, at atol = rtol = 1e-3.
 Workloads follow the acceptance configs (X, Y ~ N(0,1)/8, gamma = 0.5,
 dK ~ N(0,1)): N = M = 2048, 4096 and 8192 for seeds 0-4 (the reference
 protocol's seeds), with size-independent identities at 8192; then ragged and edge shapes, the
-generic (D != 64, misaligned) path, empty inputs, gamma = 0, the committed
+generic (D != 64, misaligned) path, empty inputs, gamma = 0, NaN inputs, the committed
 fixtures written by the reference's own CPU loops, and the framework's
 verify_all against the case's reference.
 """
@@ -124,6 +124,30 @@ def test_rbf_gamma_zero_and_self_kernel():
     assert torch.all(dX == 0) and torch.all(dY == 0)
     K2, _, _ = _run_autograd(X, X.clone(), torch.zeros(200, 200), 0.5)
     _close("diag(K(X,X))", torch.diagonal(K2), np.ones(200))
+
+
+@pytest.mark.parametrize("n,m", [(256, 256), (200, 150)])
+def test_rbf_nan_rows_propagate(n, m):
+    """A NaN in row i of X (column j of Y) makes K[i, :] (K[:, j]) NaN, as the
+    reference's exp(-gamma * sum((x - y)^2)) does: the distance clamp is a
+    compare and select, which passes NaN through (v_min / v_med3 would map it
+    to 0 and give K = 1).  Every other entry matches the oracle.  256 x 256
+    takes the full-tile kernel, 200 x 150 the ragged one."""
+    announce(f"rbf NaN rows {n}x{m}")
+    X, Y, _ = _inputs(n, m, 64, 11)
+    X[3, 5] = float("nan")
+    Y[7, 0] = float("nan")
+    K = _op().candidate({"X": X.cuda(), "Y": Y.cuda()}, {"gamma": 0.5})
+    torch.cuda.synchronize()
+    Kc = K.cpu()
+    nan_mask = torch.zeros(n, m, dtype=torch.bool)
+    nan_mask[3, :] = True
+    nan_mask[:, 7] = True
+    assert torch.equal(torch.isnan(Kc), nan_mask)
+    Kr = orbf.forward_f64(X.numpy(), Y.numpy(), 0.5)
+    assert np.array_equal(np.isnan(Kr), nan_mask.numpy())
+    keep = ~nan_mask.numpy()
+    _close("K (finite part)", Kc.numpy()[keep], Kr[keep])
 
 
 def test_rbf_empty_inputs():
