@@ -100,6 +100,30 @@ def test_layernorm_constant_rows():
     _check(x, w, b, dy)
 
 
+@pytest.mark.parametrize("b,d", [(64, 4096), (96, 1024)])
+def test_layernorm_nan_row_stays_in_its_row(b, d):
+    """A NaN in one row of x makes that row of y and dx NaN (its mean and
+    variance are NaN, as in torch's layer_norm) and, through the column sums,
+    every element of dgamma; dbeta does not involve x and stays finite.
+    The other rows match the oracle."""
+    announce(f"layernorm NaN row [{b},{d}]")
+    x, w, bias, dy = _inputs(b, d, 31)
+    x[5, 17] = float("nan")
+    y, dx, dw, db = _run(x, w, bias, dy)
+    yc, dxc = y.cpu(), dx.cpu()
+    assert torch.isnan(yc[5]).all() and torch.isnan(dxc[5]).all()
+    assert not torch.isnan(torch.cat([yc[:5], yc[6:]])).any()
+    assert not torch.isnan(torch.cat([dxc[:5], dxc[6:]])).any()
+    assert torch.isnan(dw.cpu()).all() and not torch.isnan(db.cpu()).any()
+    keep = [i for i in range(b) if i != 5]
+    xk = x[keep]
+    ry, _, _ = oln.forward_f64(xk.numpy(), w.numpy(), bias.numpy(), EPS)
+    rdx, _, rdb = oln.backward_f64(dy[keep].numpy(), xk.numpy(), w.numpy(), EPS)
+    _close("y (other rows)", yc[keep], ry)
+    _close("dx (other rows)", dxc[keep], rdx)
+    _close("dbeta", db, rdb + dy[5].double().numpy())
+
+
 def test_layernorm_param_grads_deterministic():
     announce("layernorm repeatability")
     x, w, bias, dy = _inputs(2048, 4096, 11)

@@ -4,7 +4,7 @@ equal to torch's CPU cumsum in all but a few rounding-tie elements), int32
 bit-exact.  Shapes: the acceptance workload [64, 65536], the reference's
 default [4096, 4096], ragged widths (scalar path), rows longer than 256
 chunks (multi-tile chunks), more chunks than resident workgroups (persistent
-loop), misaligned pointers, empty inputs, and full-size identities."""
+loop), misaligned pointers, empty inputs, NaN inputs, and full-size identities."""
 
 import ctypes
 
@@ -68,6 +68,33 @@ def test_scan_f32_baseline_64x65536(seed):
     torch.cuda.synchronize()
     _close("y", y, osc.cumsum_f32(x.numpy()), min_equal=0.999)
     _close("dx", xd.grad, osc.reverse_cumsum_f32(dy.numpy()), min_equal=0.999)
+
+
+def test_scan_nan_propagates_across_chunks():
+    """A NaN makes every later element of its row NaN, as torch's cumsum
+    does, also in the row's later chunks (the NaN reaches them through the
+    published chunk totals); rows without one match the oracle, and the
+    reverse scan of the backward carries it towards the row's start."""
+    announce("scan f32 NaN across chunks")
+    op = _op()
+    x = _u(4, 65536, 21)
+    x[1, 5000] = float("nan")   # inside the second 4096-element chunk
+    x[2, 65535] = float("nan")  # the last element
+    dy = torch.randn(4, 65536, generator=torch.Generator().manual_seed(22))
+    dy[3, 30000] = float("nan")
+    xd = x.cuda().requires_grad_(True)
+    y = op.candidate({"X": xd}, {})
+    y.backward(dy.cuda())
+    torch.cuda.synchronize()
+    yc, gc = y.detach().cpu(), xd.grad.cpu()
+    ref_y = torch.cumsum(x.double(), dim=1)
+    ref_g = torch.flip(torch.cumsum(torch.flip(dy.double(), [1]), dim=1), [1])
+    assert torch.equal(torch.isnan(yc), torch.isnan(ref_y))
+    assert torch.equal(torch.isnan(gc), torch.isnan(ref_g))
+    assert torch.isnan(yc[1, 5000:]).all() and not torch.isnan(yc[1, :5000]).any()
+    assert torch.isnan(gc[3, :30001]).all() and not torch.isnan(gc[3, 30001:]).any()
+    _close("y (rows 0, 3)", yc[[0, 3]], osc.cumsum_f32(x[[0, 3]].numpy()))
+    _close("dx (rows 0-2)", gc[:3], osc.reverse_cumsum_f32(dy[:3].numpy()))
 
 
 @pytest.mark.parametrize("seed", [0, 1, 2, 3, 4])
