@@ -240,6 +240,49 @@ def test_spmv_structures(kind, m, k, d):
         _check(*_csr(lens, k, d, m + d, idx))
 
 
+@pytest.mark.parametrize("d", [1, 64])
+def test_spmv_nan_propagates(d):
+    """A NaN in one row of X reaches exactly the rows of Y that use that
+    column and the dvals of those positions; a NaN in one row of dY reaches
+    exactly the dX rows of that row's columns (through the D = 1 sort and sum,
+    or the SpMM column gather) and its dvals.  Everything else matches the
+    oracle."""
+    announce(f"spmv NaN propagation D={d}")
+    from cases.spmv import op
+    rng = np.random.default_rng(41)
+    m, k = 3000, 2500
+    lens = np.minimum(rng.zipf(1.5, m), 300)
+    ptr, col, vals, X = _csr(lens, k, d, 41, torch.int32)
+    rows = np.repeat(np.arange(m), lens)
+    c0 = int(col[len(col) // 2])
+    r0 = int(rows[len(col) // 3])
+    X[c0, 0] = float("nan")
+    dY = torch.randn(m, d, generator=torch.Generator().manual_seed(42))
+    dY[r0, 0] = float("nan")
+    y = op.spmv_forward(ptr.cuda(), col.cuda(), vals.cuda(), X.cuda())
+    dv, dX = op.spmv_backward(ptr.cuda(), col.cuda(), vals.cuda(), X.cuda(), dY.cuda())
+    torch.cuda.synchronize()
+    coln = col.numpy()
+    hit_rows = np.unique(rows[coln == c0])
+    hit_cols = np.unique(coln[rows == r0])
+    ynan = torch.isnan(y.cpu()).any(dim=1).numpy()
+    assert np.array_equal(np.nonzero(ynan)[0], hit_rows)
+    xnan = torch.isnan(dX.cpu()).any(dim=1).numpy()
+    assert np.array_equal(np.nonzero(xnan)[0], hit_cols)
+    vnan = torch.isnan(dv.cpu()).numpy()
+    assert np.array_equal(vnan, (coln == c0) | (rows == r0))
+    Xc = X.clone()
+    Xc[c0, 0] = 0.0
+    dYc = dY.clone()
+    dYc[r0, 0] = 0.0
+    ry = osp.forward_f64(ptr.numpy(), coln, vals.numpy(), Xc.numpy())
+    rdv, rdX = osp.backward_f64(ptr.numpy(), coln, vals.numpy(), Xc.numpy(), dYc.numpy())
+    keep_r, keep_c = ~ynan, ~xnan
+    _close("y (other rows)", y.cpu()[keep_r], ry[keep_r])
+    _close("dX (other rows)", dX.cpu()[keep_c], rdX[keep_c])
+    _close("dvals (other positions)", dv.cpu()[~vnan], rdv[~vnan])
+
+
 def test_spmv_d1_beyond_the_bucket_sort():
     """More columns than the bucket sort covers (1024 buckets of 16384
     columns, 2^24): dX at D == 1 takes the zero-fill plus fp32 atomics route
