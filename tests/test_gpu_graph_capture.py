@@ -1,7 +1,7 @@
 """Graph capture of the launches that hand values between workgroups
 through nonce-tagged slots (the long-row scan, the softmax CE forward and
 the column offsets of the SpMM backward), and of the SpMV D = 1 forward and
-sorted backward.
+sorted backward and the RBF forward and backward.
 A captured launch keeps the nonce it was captured with, so the libraries
 clear the slots with a fill kernel captured ahead of it.  Each test replays
 one graph several times on new inputs, with eager calls and
@@ -156,3 +156,45 @@ def test_spmv_d1_graph_replays_with_new_inputs():
         ey, edv, _ = step()
         torch.cuda.synchronize()
         assert torch.equal(ey, y_s) and torch.equal(edv, dv_s), f"replay {seed}"
+
+
+def test_rbf_graph_replays_with_new_inputs():
+    """The headline RBF forward and backward (tile kernels plus the partial
+    reduce, workspace from the caching allocator) captured once and replayed
+    on new X, Y and dK: every replay equals an eager call bit for bit and
+    matches the float64 oracle."""
+    announce("rbf forward + backward graph capture (N = M = 1024)")
+    from cases.rbf import op
+    from oracle import rbf as orbf
+    n = m = 1024
+    x_s = torch.zeros(n, 64, device="cuda")
+    y_s = torch.zeros(m, 64, device="cuda")
+    g_s = torch.zeros(n, m, device="cuda")
+
+    def step():
+        xd = x_s.detach().requires_grad_(True)
+        yd = y_s.detach().requires_grad_(True)
+        k = op.candidate({"X": xd, "Y": yd}, {"gamma": 0.5})
+        dx, dy = torch.autograd.grad(k, (xd, yd), g_s)
+        return k.detach(), dx, dy
+
+    g, (k_s, dx_s, dy_s) = _capture(step)
+    for seed in range(3):
+        gen = torch.Generator().manual_seed(600 + seed)
+        X = torch.randn(n, 64, generator=gen) * 0.125
+        Y = torch.randn(m, 64, generator=gen) * 0.125
+        G = torch.randn(n, m, generator=gen)
+        x_s.copy_(X.cuda())
+        y_s.copy_(Y.cuda())
+        g_s.copy_(G.cuda())
+        g.replay()
+        torch.cuda.synchronize()
+        Kr = orbf.forward_f64(X.numpy(), Y.numpy(), 0.5)
+        dXr, dYr = orbf.backward_f64(X.numpy(), Y.numpy(), G.numpy(), Kr, 0.5)
+        for name, got, ref_ in (("K", k_s, Kr), ("dX", dx_s, dXr), ("dY", dy_s, dYr)):
+            err = np.abs(got.cpu().double().numpy() - ref_)
+            print(f"  replay {seed} {name}: max_abs={err.max():.3e}")
+            assert np.all(err <= 1e-3 + 1e-3 * np.abs(ref_)), f"replay {seed}: {name}"
+        ek, edx, edy = step()
+        torch.cuda.synchronize()
+        assert torch.equal(ek, k_s) and torch.equal(edx, dx_s) and torch.equal(edy, dy_s), seed
