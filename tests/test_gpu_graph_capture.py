@@ -1,7 +1,7 @@
 """Graph capture of the launches that hand values between workgroups
 through nonce-tagged slots (the long-row scan, the softmax CE forward and
 the column offsets of the SpMM backward), and of the SpMV D = 1 forward and
-sorted backward and the RBF forward and backward.
+sorted backward, the RBF forward and backward, and LayerNorm.
 A captured launch keeps the nonce it was captured with, so the libraries
 clear the slots with a fill kernel captured ahead of it.  Each test replays
 one graph several times on new inputs, with eager calls and
@@ -198,3 +198,47 @@ def test_rbf_graph_replays_with_new_inputs():
         ek, edx, edy = step()
         torch.cuda.synchronize()
         assert torch.equal(ek, k_s) and torch.equal(edx, dx_s) and torch.equal(edy, dy_s), seed
+
+
+@pytest.mark.parametrize("b,d", [(512, 4096), (300, 1000)])
+def test_layernorm_graph_replays_with_new_inputs(b, d):
+    """LayerNorm forward and backward (row kernels and the column sums; the
+    generic path at D = 1000) captured once and replayed on new inputs: every
+    replay equals an eager call bit for bit and matches the float64 oracle."""
+    announce(f"layernorm graph capture [{b},{d}]")
+    from cases.layernorm import op
+    from oracle import layernorm as oln
+    eps = 1e-5
+    x_s = torch.zeros(b, d, device="cuda")
+    w_s = torch.ones(d, device="cuda")
+    bias_s = torch.zeros(d, device="cuda")
+    dy_s = torch.zeros(b, d, device="cuda")
+
+    def step():
+        xd = x_s.detach().requires_grad_(True)
+        wd = w_s.detach().requires_grad_(True)
+        bd = bias_s.detach().requires_grad_(True)
+        y = op.candidate({"X": xd, "gamma": wd, "beta": bd}, {"eps": eps})
+        grads = torch.autograd.grad(y, (xd, wd, bd), dy_s)
+        return (y.detach(),) + tuple(grads)
+
+    g, outs = _capture(step)
+    for seed in range(3):
+        gen = torch.Generator().manual_seed(700 + seed)
+        x = torch.randn(b, d, generator=gen)
+        w = 1 + 0.1 * torch.randn(d, generator=gen)
+        bias = 0.1 * torch.randn(d, generator=gen)
+        dy = torch.randn(b, d, generator=gen)
+        for dst, src in ((x_s, x), (w_s, w), (bias_s, bias), (dy_s, dy)):
+            dst.copy_(src.cuda())
+        g.replay()
+        torch.cuda.synchronize()
+        ry, _, _ = oln.forward_f64(x.numpy(), w.numpy(), bias.numpy(), eps)
+        rdx, rdw, rdb = oln.backward_f64(dy.numpy(), x.numpy(), w.numpy(), eps)
+        for name, got, ref_ in zip(("y", "dx", "dw", "db"), outs, (ry, rdx, rdw, rdb)):
+            err = np.abs(got.cpu().double().numpy() - ref_)
+            print(f"  replay {seed} {name}: max_abs={err.max():.3e}")
+            assert np.all(err <= 1e-3 + 1e-3 * np.abs(ref_)), f"replay {seed}: {name}"
+        eager = step()
+        torch.cuda.synchronize()
+        assert all(torch.equal(e, o) for e, o in zip(eager, outs)), seed
