@@ -235,7 +235,10 @@ def spmv(dev, time_us):
     return out
 
 
-def cosine(dev, time_us):
+COSINE_SIZES = (2048, 4096)
+
+
+def cosine(dev, time_us, sizes=COSINE_SIZES):
     """Pairwise cosine similarity (fp32 MFMA-bound): flops = 2NMD forward,
     4NMD backward; bytes = each input read once, each output written once."""
     import torch
@@ -243,7 +246,7 @@ def cosine(dev, time_us):
     from cases.cosine_sim import op
     lib = op._lib()
     out = []
-    for n in (2048, 4096):
+    for n in sizes:
         D = 64
         g = torch.Generator().manual_seed(0)
         A = torch.randn(n, D, generator=g).to(dev)
@@ -276,6 +279,8 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--scan-shape", default=None, metavar="RxD",
                     help="time only this scan shape (default: 64x65536 and 4096x4096)")
+    ap.add_argument("--cosine-size", type=int, default=None, metavar="N",
+                    help="time only N x N cosine similarity (default: 2048 and 4096)")
     ns = ap.parse_args(argv)
     import torch
     dev = torch.device("cuda:0")
@@ -285,9 +290,10 @@ def main(argv=None):
     if ns.scan_shape:
         r, d = (int(v) for v in ns.scan_shape.lower().split("x"))
         scan_shapes = ((r, d),)
+    cos_sizes = (ns.cosine_size,) if ns.cosine_size else COSINE_SIZES
     cases = {"layernorm": layernorm, "l2norm": l2norm,
-             "scan": lambda dv, t: scan(dv, t, scan_shapes), "spmv": spmv, "cosine": cosine,
-             "softmax_ce": softmax_ce}
+             "scan": lambda dv, t: scan(dv, t, scan_shapes), "spmv": spmv,
+             "cosine": lambda dv, t: cosine(dv, t, cos_sizes), "softmax_ce": softmax_ce}
     rows = []
     for name in (cases if ns.case == "all" else [ns.case]):
         for case, what, t, nbytes, detail, *flops in cases[name](dev, time_us):
