@@ -88,15 +88,25 @@ def repeat_stats(samples, repeats=3):
 
 
 def cpu_info():
-    model = "unknown"
+    """(CPU description, CPUs this process may run on).  The description is
+    /proc/cpuinfo's model name with its family / model / stepping numbers
+    (a virtualised host may report only "AMD EPYC" as the name) and the
+    machine's logical CPU count."""
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
+                if not line.strip():
+                    break  # the first processor's block is enough
+                k, _, v = line.partition(":")
+                fields.setdefault(k.strip(), v.strip())
     except OSError:
         pass
+    model = fields.get("model name", "unknown")
+    ids = [f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields]
+    if ids:
+        model += " (" + ", ".join(ids) + ")"
+    model += f", {os.cpu_count()} logical CPUs"
     try:
         share = len(os.sched_getaffinity(0))
     except AttributeError:
@@ -266,8 +276,18 @@ def run_rbf_config(n, iters, warmup, seeds, cpu):
             t_bwd = timer.us(g.bwd, iters, warmup)
         if cpu:
             merge_errors(errs, cpu_rbf_errors(X, Y, dK, out, g.gamma))
-            if n <= 2048:
-                cpu_ref = cpu_rbf_reference(X, Y, dK, out, g.gamma, cpu_ref)
+            # The reference's CPU path at full size: every seed at 2048, the
+            # first seed above it (seconds per call), unless the host cannot
+            # hold its [N, M, D] intermediates.
+            if n <= 2048 or seed == seeds[0]:
+                need = rbf_cpu_reference_bytes(n, n, g.d)
+                avail = host_mem_available()
+                if avail is not None and need > 0.8 * avail:
+                    cpu_ref = {"skipped": (f"OOM: the torch CPU reference needs about "
+                                           f"{need / 2**30:.0f} GiB of host memory at N=M={n}, "
+                                           f"D={g.d}; MemAvailable is {avail / 2**30:.0f} GiB")}
+                else:
+                    cpu_ref = cpu_rbf_reference(X, Y, dK, out, g.gamma, cpu_ref)
     name = f"rbf N=M={n} D=64"
     common = {"seeds": list(seeds)}
     fe = _entry(name, "forward", t_fwd, fb, ff, "mfma", dict(common))
@@ -275,10 +295,33 @@ def run_rbf_config(n, iters, warmup, seeds, cpu):
     if errs:
         fe["outputs"] = {"K": errs["K"]}
         be["outputs"] = {"dX": errs["dX"], "dY": errs["dY"]}
-    if cpu_ref:
+    if cpu_ref and "skipped" in cpu_ref:
+        fe["cpu_reference"] = be["cpu_reference"] = dict(cpu_ref)
+    elif cpu_ref:
         fe["cpu_reference"] = cpu_ref["fwd"]
         be["cpu_reference"] = cpu_ref["bwd"]
+        for e in (fe["cpu_reference"], be["cpu_reference"]):
+            e["seeds"] = list(seeds) if n <= 2048 else [seeds[0]]
     return [fe, be], errs
+
+
+def rbf_cpu_reference_bytes(n, m, d):
+    """Peak host memory of the reference's CPU broadcast path with autograd:
+    the [n, m, d] difference, its square and their gradients (four fp32
+    [n, m, d] arrays at once)."""
+    return 4 * 4 * n * m * d
+
+
+def host_mem_available():
+    """MemAvailable of /proc/meminfo in bytes (None where it cannot be read)."""
+    try:
+        with open("/proc/meminfo") as f:
+            for line in f:
+                if line.startswith("MemAvailable:"):
+                    return int(line.split()[1]) * 1024
+    except (OSError, ValueError, IndexError):
+        pass
+    return None
 
 
 def run_layernorm_config(iters, warmup, cpu):

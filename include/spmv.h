@@ -10,9 +10,13 @@
  * Dense arrays are row-major fp32 device arrays owned by the caller; kernels
  * run on `stream`; nothing is allocated and no state is kept.  Preconditions
  * on the structure (row_ptr[0] = 0, non-decreasing, row_ptr[M] = nnz,
- * 0 <= col_idx < K) cannot be checked without reading device memory; the
- * kernels clamp every index they load into range, so a malformed structure
- * gives wrong numbers, never an out-of-bounds access.  The forward and
+ * 0 <= col_idx < K) are not checked by the product entry points, which
+ * would need a read-back of device memory; their kernels clamp every index
+ * they load into range, so a malformed structure gives wrong numbers, never
+ * an out-of-bounds access.  spmv_check_structure_* below checks them on the
+ * device for a caller that wants the reference's error (op.py runs it when
+ * NL2K_CHECK=1 and raises IndexError for a column out of range, as the
+ * reference's index_select does, RuntimeError for a bad row_ptr).  The forward and
  * dvals are deterministic; the D == 1 forward's order of additions does not
  * depend on how rows are split between waves (which follows the device's CU
  * count), so it gives the same bits on any device.  At D > 1 with K <= 16384 (the reference's
@@ -115,6 +119,21 @@ int spmv_backward_gathered_f32_i64(const int64_t* row_ptr, const int64_t* col_id
                                    const float* dY, float* dvals, float* dX, int64_t M,
                                    int64_t K, int64_t D, int64_t nnz, void* workspace,
                                    size_t workspace_bytes, hipStream_t stream);
+
+/* Structure check: report[4] (uint64, 16-byte aligned, device memory) gets
+ * report[0] = OR of 1 (row_ptr[0] != 0), 2 (row_ptr decreasing or outside
+ * [0, nnz]), 4 (row_ptr[M] != nnz), 8 (a column outside [0, K)); report[1] =
+ * the first position p with col_idx[p] out of range (UINT64_MAX if none);
+ * report[2] = the first r whose row_ptr[r] is bad (UINT64_MAX if none);
+ * report[3] = 0.  Two kernels on `stream`, no read-back: the caller reads
+ * the report after the stream.  No counterpart in the reference kernels
+ * (spmv.cu:199-288 read the structure unchecked); it stands in for the
+ * IndexError of the reference path's X.index_select(0, col_idx)
+ * (cases/spmv/reference.py:19). */
+int spmv_check_structure_i32(const int32_t* row_ptr, const int32_t* col_idx, int64_t M,
+                             int64_t K, int64_t nnz, uint64_t* report, hipStream_t stream);
+int spmv_check_structure_i64(const int64_t* row_ptr, const int64_t* col_idx, int64_t M,
+                             int64_t K, int64_t nnz, uint64_t* report, hipStream_t stream);
 
 const char* spmv_last_error(void);
 

@@ -1563,6 +1563,48 @@ __global__ __launch_bounds__(kThreads) void spmv_fill_zero_kernel(float* __restr
     a[i] = 0.f;
 }
 
+// Structure check (spmv_check_structure_*): report[0] collects the
+// kStruct* bits of every violation, report[1] the smallest position whose
+// column is out of [0, K), report[2] the smallest r with a bad row_ptr[r]
+// (r = 0 for row_ptr[0] != 0, r = M for row_ptr[M] != nnz, else the first
+// r with row_ptr[r] < row_ptr[r-1] or outside [0, nnz]).  The two kernels
+// run in stream order: the first sets the report's initial values (no
+// memset, so the pair can be captured into a HIP graph).
+constexpr unsigned long long kStructFirst = 1, kStructOrder = 2, kStructLast = 4,
+                             kStructColumn = 8;
+
+__global__ void spmv_check_init_kernel(unsigned long long* __restrict__ report) {
+  if (threadIdx.x < 4) report[threadIdx.x] = threadIdx.x == 0 || threadIdx.x == 3 ? 0ull : ~0ull;
+}
+
+template <typename I>
+__global__ __launch_bounds__(kThreads) void spmv_check_kernel(
+    const I* __restrict__ ptr, const I* __restrict__ col, int64_t M, int64_t K, int64_t nnz,
+    unsigned long long* __restrict__ report) {
+  const int64_t n = std::max<int64_t>(M + 1, nnz);
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kThreads) {
+    if (i <= M) {
+      const int64_t v = (int64_t)ptr[i];
+      unsigned long long bad = 0;
+      if (i == 0 && v != 0) bad |= kStructFirst;
+      if (i == M && v != nnz) bad |= kStructLast;
+      if (v < 0 || v > nnz || (i > 0 && v < (int64_t)ptr[i - 1])) bad |= kStructOrder;
+      if (bad) {
+        atomicOr(&report[0], bad);
+        atomicMin(&report[2], (unsigned long long)i);
+      }
+    }
+    if (i < nnz) {
+      const int64_t c = (int64_t)col[i];
+      if (c < 0 || c >= K) {
+        atomicOr(&report[0], kStructColumn);
+        atomicMin(&report[1], (unsigned long long)i);
+      }
+    }
+  }
+}
+
 // ----------------------------------------------------------------- host side
 int validate(int64_t M, int64_t K, int64_t D, int64_t nnz, int64_t index_max, const char* who) {
   if (M < 0 || K < 1 || D < 1 || nnz < 0)
@@ -1980,11 +2022,45 @@ int backward(const I* ptr, const I* col, const float* vals, const float* X, cons
   return nl2k::check_launch(who);
 }
 
+template <typename I>
+int check_structure(const I* ptr, const I* col, int64_t M, int64_t K, int64_t nnz,
+                    unsigned long long* report, hipStream_t stream, const char* who) {
+  const int64_t imax = sizeof(I) == 4 ? INT32_MAX : INT64_MAX / 2;
+  int st = validate(M, K, 1, nnz, imax, who);
+  if (st) return st;
+  if (!ptr || !report || (nnz > 0 && !col))
+    return nl2k::fail(NL2K_ERR_NULL, "%s: row_ptr, col_idx and report must be non-null", who);
+  if (!nl2k::aligned16(report))
+    return nl2k::fail(NL2K_ERR_ALIGN, "%s: report must be 16-byte aligned", who);
+  hipLaunchKernelGGL(spmv_check_init_kernel, dim3(1), dim3(64), 0, stream, report);
+  st = nl2k::check_launch(who);
+  if (st) return st;
+  const int64_t n = std::max<int64_t>(M + 1, nnz);
+  const int blocks = (int)std::min<int64_t>(nl2k::ceil_div(n, (int64_t)kThreads), 4096);
+  hipLaunchKernelGGL(spmv_check_kernel<I>, dim3(blocks), dim3(kThreads), 0, stream, ptr, col, M,
+                     K, nnz, report);
+  return nl2k::check_launch(who);
+}
+
 }  // namespace
 
 extern "C" {
 
 const char* spmv_last_error(void) { return nl2k::error_slot().text; }
+
+int spmv_check_structure_i32(const int32_t* row_ptr, const int32_t* col_idx, int64_t M,
+                             int64_t K, int64_t nnz, uint64_t* report, hipStream_t stream) {
+  return check_structure(row_ptr, col_idx, M, K, nnz,
+                         reinterpret_cast<unsigned long long*>(report), stream,
+                         "spmv_check_structure_i32");
+}
+
+int spmv_check_structure_i64(const int64_t* row_ptr, const int64_t* col_idx, int64_t M,
+                             int64_t K, int64_t nnz, uint64_t* report, hipStream_t stream) {
+  return check_structure(row_ptr, col_idx, M, K, nnz,
+                         reinterpret_cast<unsigned long long*>(report), stream,
+                         "spmv_check_structure_i64");
+}
 
 int spmv_forward_f32_i32(const int32_t* row_ptr, const int32_t* col_idx, const float* vals,
                          const float* X, float* Y, int64_t M, int64_t K, int64_t D,

@@ -1,16 +1,25 @@
 """CSR SpMM / SpMV candidate: autograd wrapper over libspmv_hip.so.
 
 Mirrors the reference's cases/spmv/op.py:24-57: ``_CSRSpMMFunction`` saves
-(row_ptr, col_idx, vals, X) (plus, at D == 1 when vals needs a gradient,
-the gathered X[col_idx] the forward read) and returns (None, None,
-grad_vals, grad_X);
-``candidate`` / ``forward_only`` keep the dict interface.  The argument
-checks follow spmv.cu:167-197 (GPU tensors, fp32 values, 1-D structure of
-matching lengths, rank-2 X with positive sizes), with int32 indices accepted
-beside int64 (row_ptr and col_idx must share the type).  There is no CPU
-path: without a GPU the library refuses to load.  With ``NL2K_CHECK=1``
-the backward also zeroes and reads back the workspace's trip counter (a
-synchronisation) on shapes that build the column-major copy of A.
+exactly (row_ptr, col_idx, vals, X) and returns (None, None, grad_vals,
+grad_X); ``candidate`` / ``forward_only`` keep the dict interface.  The
+argument checks follow spmv.cu:167-197 (GPU tensors, fp32 values, 1-D
+structure of matching lengths, rank-2 X with positive sizes), with int32
+indices accepted beside int64 (row_ptr and col_idx must share the type).
+There is no CPU path: without a GPU the library refuses to load.
+
+Opt-in (``params["keep_gather"] = True`` or ``NL2K_SPMV_KEEP_GATHER=1``):
+at D == 1 with vals requiring grad, ``_CSRSpMMKeepGatherFunction`` also
+saves the gathered X[col_idx] the forward read (nnz floats), so the
+backward's dvals streams it instead of gathering X again; gradients are
+bit-identical, the forward writes nnz * 4 more bytes.
+
+With ``NL2K_CHECK=1`` every call first checks the CSR structure on the
+device and reads the report back (a synchronisation): a column outside
+[0, K) raises IndexError, as the reference path's ``X.index_select(0,
+col_idx)`` does (cases/spmv/reference.py:19), and a malformed row_ptr
+raises RuntimeError; the backward also zeroes and reads back the
+workspace's trip counter on shapes that build the column-major copy of A.
 """
 
 import ctypes
@@ -37,6 +46,7 @@ def bind_library(lib):
                   [V, V, V, V, V, V, V, I64, I64, I64, I64, V, capi.c_size_t, V])
         capi.bind(lib, f"spmv_backward_gathered_f32_{t}",
                   [V, V, V, V, V, V, V, V, I64, I64, I64, I64, V, capi.c_size_t, V])
+        capi.bind(lib, f"spmv_check_structure_{t}", [V, V, I64, I64, I64, V, V])
     capi.bind(lib, "spmv_backward_workspace_bytes", [I64, I64, I64, I64], restype=capi.c_size_t)
     capi.bind(lib, "spmv_status_offset", [I64, I64, I64, I64], restype=capi.c_size_t)
     capi.bind_last_error(lib, "spmv_last_error")
@@ -68,6 +78,37 @@ def _validate(row_ptr, col_idx, vals, X):
     return _suffix(row_ptr, col_idx)
 
 
+def check_structure(row_ptr, col_idx, K):
+    """Checks the CSR structure on the device (one read-back) and raises
+    what the reference path would: IndexError for a column outside [0, K),
+    RuntimeError for a row_ptr that does not start at 0, decreases or does
+    not end at nnz."""
+    t = _suffix(row_ptr, col_idx)
+    lib = _lib()
+    M, nnz = row_ptr.numel() - 1, col_idx.numel()
+    report = torch.empty(4, dtype=torch.int64, device=row_ptr.device)
+    with torch.cuda.device(row_ptr.device):
+        st = getattr(lib, f"spmv_check_structure_{t}")(
+            capi.ptr(row_ptr), capi.ptr(col_idx), M, K, nnz, capi.ptr(report),
+            capi.stream_of(row_ptr))
+    capi.check(st, lib.spmv_last_error, "spmv_check_structure")
+    flags, bad_pos, bad_row, _ = (v & 0xFFFFFFFFFFFFFFFF for v in report.cpu().tolist())
+    if flags & 8:
+        c = int(col_idx[bad_pos].item())
+        raise IndexError(f"spmv: index out of range: col_idx[{bad_pos}] = {c} is not in "
+                         f"[0, {K}) (X has {K} rows)")
+    if flags:
+        what = []
+        if flags & 1:
+            what.append("row_ptr[0] != 0")
+        if flags & 2:
+            what.append("row_ptr decreases or leaves [0, nnz]")
+        if flags & 4:
+            what.append(f"row_ptr[M] != nnz ({nnz})")
+        raise RuntimeError(f"spmv: malformed CSR structure: {', '.join(what)} "
+                           f"(first at row_ptr[{bad_row}])")
+
+
 def spmv_forward(row_ptr, col_idx, vals, X, keep_gather=False):
     """Y = A X.  keep_gather=True (D == 1 only) also returns Xg [nnz] =
     X[col_idx] as the kernel read it, for spmv_backward(..., X_gathered=Xg)."""
@@ -76,6 +117,8 @@ def spmv_forward(row_ptr, col_idx, vals, X, keep_gather=False):
     row_ptr, col_idx, vals, X = (a.contiguous() for a in (row_ptr, col_idx, vals, X))
     M = row_ptr.numel() - 1
     K, D = X.shape
+    if capi.checking() and not torch.cuda.is_current_stream_capturing():
+        check_structure(row_ptr, col_idx, K)
     Y = torch.empty((M, D), dtype=torch.float32, device=X.device)
     if keep_gather:
         capi.require(D == 1, "keep_gather needs D == 1")
@@ -111,6 +154,8 @@ def spmv_backward(row_ptr, col_idx, vals, X, grad_Y, need_vals=True, need_X=True
     lib = _lib()
     row_ptr, col_idx, vals, X, grad_Y = (a.contiguous() for a in (row_ptr, col_idx, vals, X, grad_Y))
     K, D = X.shape
+    if capi.checking() and not torch.cuda.is_current_stream_capturing():
+        check_structure(row_ptr, col_idx, K)
     grad_vals = torch.empty_like(vals) if need_vals else None
     grad_X = torch.empty_like(X) if need_X else None
     ws_bytes = lib.spmv_backward_workspace_bytes(M, K, D, vals.numel()) if need_X else 0
@@ -141,10 +186,35 @@ def spmv_backward(row_ptr, col_idx, vals, X, grad_Y, need_vals=True, need_X=True
 
 
 class _CSRSpMMFunction(torch.autograd.Function):
-    """At D == 1 with vals requiring grad, the forward also keeps X[col_idx]
-    (nnz floats), so the backward's dvals streams it instead of gathering X
-    (the random reads that bound the D == 1 walk); gradients are
-    bit-identical either way."""
+    """The reference's autograd contract (cases/spmv/op.py:24-40): saves
+    (row_ptr, col_idx, vals, X); backward returns (None, None, grad_vals,
+    grad_X)."""
+
+    @staticmethod
+    def forward(ctx, row_ptr, col_idx, vals, X):
+        row_ptr = row_ptr.contiguous()
+        col_idx = col_idx.contiguous()
+        vals = vals.contiguous()
+        X = X.contiguous()
+        Y = spmv_forward(row_ptr, col_idx, vals, X)
+        ctx.save_for_backward(row_ptr, col_idx, vals, X)
+        return Y
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        row_ptr, col_idx, vals, X = ctx.saved_tensors
+        grad_vals, grad_X = spmv_backward(row_ptr, col_idx, vals, X, grad_output.contiguous(),
+                                          need_vals=ctx.needs_input_grad[2],
+                                          need_X=ctx.needs_input_grad[3])
+        return None, None, grad_vals, grad_X
+
+
+class _CSRSpMMKeepGatherFunction(torch.autograd.Function):
+    """Opt-in variant (no counterpart in the reference): at D == 1 with vals
+    requiring grad the forward also saves Xg = X[col_idx] as it read it, a
+    fifth saved tensor of nnz floats, and the backward's dvals streams Xg
+    instead of gathering X; gradients are bit-identical to
+    _CSRSpMMFunction's.  Other shapes save the reference's four tensors."""
 
     @staticmethod
     def forward(ctx, row_ptr, col_idx, vals, X):
@@ -171,9 +241,17 @@ class _CSRSpMMFunction(torch.autograd.Function):
         return None, None, grad_vals, grad_X
 
 
+def keep_gather_requested(params=None):
+    """The opt-in of _CSRSpMMKeepGatherFunction: params["keep_gather"], else
+    NL2K_SPMV_KEEP_GATHER=1 in the environment."""
+    if params and "keep_gather" in params:
+        return bool(params["keep_gather"])
+    return os.environ.get("NL2K_SPMV_KEEP_GATHER", "") == "1"
+
+
 def candidate(inputs, params):
-    del params
-    return _CSRSpMMFunction.apply(inputs["row_ptr"], inputs["col_idx"], inputs["vals"], inputs["X"])
+    fn = _CSRSpMMKeepGatherFunction if keep_gather_requested(params) else _CSRSpMMFunction
+    return fn.apply(inputs["row_ptr"], inputs["col_idx"], inputs["vals"], inputs["X"])
 
 
 def forward_only(inputs, params):

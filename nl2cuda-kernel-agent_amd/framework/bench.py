@@ -21,8 +21,8 @@ reference; ``baseline="eager"`` times the eager reference instead.
 
 import math
 import os
-import statistics
 import sys
+from dataclasses import dataclass
 
 sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
 
@@ -81,61 +81,71 @@ def time_ms(fn, warmup=None, iters=None, flush=True, setup=None, device="cuda"):
     return times
 
 
-def _summarize(kind, geomeans, cv_threshold):
-    mean = statistics.mean(geomeans)
-    cv = (statistics.pstdev(geomeans) / mean) if mean > 0 else float("inf")
-    return {"kind": kind, "geomeans_ms": geomeans, "geomean_ms": _geomean(geomeans),
-            "cv": cv, "ok": cv <= cv_threshold}
+@dataclass
+class Timing:
+    """One stable measurement of a call: ``rounds_ms`` holds the geometric
+    mean of each round of ``PROTOCOL.iters`` timed iterations; ``center_ms``
+    is their geometric mean and ``cv`` their coefficient of variation.  The
+    measurement is ``stable`` when cv <= PROTOCOL.cv_threshold; ``tries``
+    counts the measurements taken to get there (at most max_retries + 1)."""
+    label: str
+    rounds_ms: list
+    center_ms: float
+    cv: float
+    stable: bool
+    tries: int = 1
 
 
-def _collect_with_retry(kind, one_round):
+def spread(values):
+    """Population coefficient of variation (inf for a non-positive mean)."""
+    m = sum(values) / len(values)
+    if m <= 0:
+        return float("inf")
+    return math.sqrt(sum((v - m) ** 2 for v in values) / len(values)) / m
+
+
+def until_stable(label, measure_round, rounds=None, cv_limit=None, retries=None):
+    """Measure ``rounds`` rounds (``measure_round()`` returns one round's
+    per-iteration times) and repeat the whole measurement while their
+    geomeans spread by more than ``cv_limit``, at most ``retries`` extra
+    times.  Returns the Timing with the lowest spread seen, so an unstable
+    result is still the best one the retries produced."""
     p = PROTOCOL
-    best = None
-    for attempt in range(p.max_retries + 1):
-        s = _summarize(kind, one_round(), p.cv_threshold)
-        s["attempts"] = attempt + 1
-        if best is None or s["cv"] < best["cv"]:
-            best = s
-        if s["ok"]:
+    rounds = p.repeats if rounds is None else rounds
+    cv_limit = p.cv_threshold if cv_limit is None else cv_limit
+    retries = p.max_retries if retries is None else retries
+    kept = None
+    for n in range(1, retries + 2):
+        centers = [_geomean(measure_round()) for _ in range(rounds)]
+        t = Timing(label, centers, _geomean(centers), spread(centers), False, n)
+        t.stable = t.cv <= cv_limit
+        if kept is None or t.cv < kept.cv:
+            kept = t
+        if t.stable:
             break
-    return best
+    kept.tries = n
+    return kept
 
 
-def forward_geomean_cv(fn, inputs, params, flush=True):
-    p = PROTOCOL
-    detached = {k: v.detach() for k, v in inputs.items()}
+def time_forward(fn, inputs, params, flush=True):
+    """Forward calls under no_grad on detached inputs."""
+    frozen = {k: v.detach() for k, v in inputs.items()}
 
-    def step():
+    def call():
         with torch.no_grad():
-            fn(detached, params)
-
-    def one_round():
-        return [_geomean(time_ms(step, p.warmup, p.iters, flush)) for _ in range(p.repeats)]
-
-    return _collect_with_retry("forward", one_round)
+            fn(frozen, params)
+    return until_stable("forward", lambda: time_ms(call, flush=flush))
 
 
-def backward_geomean_cv(fn, inputs, params, grad_inputs, G, flush=True):
-    p = PROTOCOL
-
-    def build_graph():
-        loc = {}
-        for k, v in inputs.items():
-            t = v.detach().clone()
-            if k in grad_inputs:
-                t.requires_grad_(True)
-            loc[k] = t
-        out = fn(loc, params)
-
-        def do_bwd():
-            out.backward(G)
-        return do_bwd
-
-    def one_round():
-        return [_geomean(time_ms(None, p.warmup, p.iters, flush, setup=build_graph))
-                for _ in range(p.repeats)]
-
-    return _collect_with_retry("backward", one_round)
+def time_backward(fn, inputs, params, grad_inputs, G, flush=True):
+    """``out.backward(G)`` alone: each iteration first rebuilds the forward
+    graph on fresh leaf copies, outside the timed region."""
+    def fresh_graph():
+        leaves = {k: v.detach().clone().requires_grad_(k in grad_inputs)
+                  for k, v in inputs.items()}
+        out = fn(leaves, params)
+        return lambda: out.backward(G)
+    return until_stable("backward", lambda: time_ms(None, flush=flush, setup=fresh_graph))
 
 
 def compare(case, candidate, device=None, seed=0, baseline="compile", flush=True):
@@ -162,32 +172,31 @@ def compare(case, candidate, device=None, seed=0, baseline="compile", flush=True
     results = {}
     with_bwd = len(case.grad_inputs) > 0
     for name, fn in [(base_name, base_fn), ("candidate", candidate)]:
-        fres = forward_geomean_cv(fn, inputs, case.params, flush)
-        bres = backward_geomean_cv(fn, inputs, case.params, case.grad_inputs, G, flush) \
+        fres = time_forward(fn, inputs, case.params, flush)
+        bres = time_backward(fn, inputs, case.params, case.grad_inputs, G, flush) \
             if with_bwd else None
         results[name] = (fres, bres)
         lines.append(f"\n[{name}]")
-        lines.append(f"  forward : {fres['geomean_ms']:.4f} ms  CV={fres['cv']*100:.2f}%  "
-                     f"x{fres['attempts']}  {'ok' if fres['ok'] else 'CV over threshold'}")
-        if bres:
-            lines.append(f"  backward: {bres['geomean_ms']:.4f} ms  CV={bres['cv']*100:.2f}%  "
-                         f"x{bres['attempts']}  {'ok' if bres['ok'] else 'CV over threshold'}")
+        for t in (fres, bres):
+            if t is not None:
+                lines.append(f"  {t.label:<8}: {t.center_ms:.4f} ms  CV={t.cv * 100:.2f}%  "
+                             f"x{t.tries}  {'ok' if t.stable else 'CV over threshold'}")
 
     bf, bb = results[base_name]
     cf, cb = results["candidate"]
-    fwd_speedup = bf["geomean_ms"] / cf["geomean_ms"]
+    fwd_speedup = bf.center_ms / cf.center_ms
     lines.append("\n[speedup candidate vs baseline]")
     lines.append(f"  forward : {fwd_speedup:.4f}x  (target >={p.speedup_target}x) "
                  f"{'PASS' if fwd_speedup >= p.speedup_target else 'FAIL'}")
     passed = fwd_speedup >= p.speedup_target
     cvs = [bf, cf]
     if with_bwd:
-        bwd_speedup = bb["geomean_ms"] / cb["geomean_ms"]
+        bwd_speedup = bb.center_ms / cb.center_ms
         lines.append(f"  backward: {bwd_speedup:.4f}x  (target >={p.speedup_target}x) "
                      f"{'PASS' if bwd_speedup >= p.speedup_target else 'FAIL'}")
         passed = passed and bwd_speedup >= p.speedup_target
         cvs += [bb, cb]
-    cv_ok = all(r["ok"] for r in cvs)
+    cv_ok = all(r.stable for r in cvs)
     passed = passed and cv_ok
     if not cv_ok:
         lines.append("  CV > 5% present: result invalid, re-measure")

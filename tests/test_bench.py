@@ -58,3 +58,28 @@ def test_errors_use_relative_error_only_above_atol():
     bench.merge_errors(acc, {"K": e})
     bench.merge_errors(acc, {"K": {"max_abs": 1.0, "max_rel": 0.1, "allclose": False}})
     assert acc["K"] == {"max_abs": 1.0, "max_rel": 0.1, "allclose": False}
+
+
+def test_until_stable_retries_while_the_rounds_spread_and_keeps_the_steadiest():
+    from framework.bench import spread, until_stable
+    assert spread([2.0, 2.0]) == 0.0
+    assert abs(spread([1.0, 3.0]) - 0.5) < 1e-12
+    # Two noisy measurements (round geomeans 1, 2, 1 and 1, 1.2, 1), then a
+    # steady one: three tries, the steady result kept.
+    rounds = iter([[1.0], [2.0], [1.0], [1.0], [1.2], [1.0], [4.0], [4.0], [4.1]])
+    t = until_stable("forward", lambda: next(rounds), rounds=3, cv_limit=0.05, retries=4)
+    assert t.stable and t.tries == 3
+    assert t.rounds_ms == [4.0, 4.0, 4.1]
+    assert abs(t.center_ms - (4.0 * 4.0 * 4.1) ** (1 / 3)) < 1e-12
+
+
+def test_until_stable_gives_up_after_the_retries_with_the_lowest_spread():
+    from framework.bench import until_stable
+    noisy = [[1.0], [3.0], [1.0], [1.0], [1.5], [1.0], [1.0], [4.0], [1.0]]
+    rounds = iter(noisy)
+    t = until_stable("backward", lambda: next(rounds), rounds=3, cv_limit=0.05, retries=2)
+    assert not t.stable and t.tries == 3
+    assert t.rounds_ms == [1.0, 1.5, 1.0]  # the second try spread least
+    # one round's per-iteration times enter as their geometric mean
+    t = until_stable("forward", lambda: [1.0, 4.0], rounds=2, cv_limit=0.05, retries=0)
+    assert t.stable and abs(t.center_ms - 2.0) < 1e-12

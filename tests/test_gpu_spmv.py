@@ -325,17 +325,29 @@ def test_spmv_misaligned_values():
     _close("y (misaligned X)", y, osp.forward_f64(ptr.numpy(), col.numpy(), vals.numpy(), X.numpy()))
 
 
-def test_spmv_autograd_keeps_gathered_x_at_d1():
-    """Through autograd at D == 1 with vals requiring grad the forward keeps
-    X[col] and the backward streams it: both gradients match the oracle and
-    the plain C-ABI backward."""
-    announce("spmv autograd D=1 with the gathered copy of X")
+@pytest.mark.parametrize("opt_in", ["default", "params", "env"])
+def test_spmv_autograd_saved_tensors_and_gathered_opt_in(opt_in, monkeypatch):
+    """The reference's save list (cases/spmv/op.py:28-33) by default: exactly
+    (row_ptr, col_idx, vals, X).  With the opt-in (params["keep_gather"] or
+    NL2K_SPMV_KEEP_GATHER=1) at D == 1 with vals requiring grad the forward
+    also keeps X[col] and the backward streams it.  Either way both
+    gradients match the oracle and dvals equals the plain C-ABI backward's
+    bit for bit."""
+    announce(f"spmv autograd D=1 save list ({opt_in})")
     from cases.spmv import op
+    params = {"keep_gather": True} if opt_in == "params" else {}
+    if opt_in == "env":
+        monkeypatch.setenv("NL2K_SPMV_KEEP_GATHER", "1")
     ptr, col, vals, X = _csr(np.minimum(np.random.default_rng(6).zipf(1.5, 5000), 3000), 3000, 1, 12)
     vd = vals.cuda().requires_grad_(True)
     Xd = X.cuda().requires_grad_(True)
-    y = op.candidate({"row_ptr": ptr.cuda(), "col_idx": col.cuda(), "vals": vd, "X": Xd}, {})
-    assert len(y.grad_fn.saved_tensors) == 5  # row_ptr, col_idx, vals, X, Xg
+    y = op.candidate({"row_ptr": ptr.cuda(), "col_idx": col.cuda(), "vals": vd, "X": Xd}, params)
+    saved = y.grad_fn.saved_tensors
+    if opt_in == "default":
+        assert len(saved) == 4  # row_ptr, col_idx, vals, X
+    else:
+        assert len(saved) == 5  # row_ptr, col_idx, vals, X, Xg
+        assert torch.equal(saved[4].cpu(), X[:, 0][col.long()])
     dY = torch.randn(y.shape, generator=torch.Generator().manual_seed(7))
     y.backward(dY.cuda())
     dv, _ = op.spmv_backward(ptr.cuda(), col.cuda(), vals.cuda(), X.cuda(), dY.cuda(), need_X=False)
@@ -344,6 +356,60 @@ def test_spmv_autograd_keeps_gathered_x_at_d1():
     _close("dvals", vd.grad, rdv)
     _close("dX", Xd.grad, rdX)
     assert torch.equal(vd.grad, dv)
+
+
+def test_spmv_opt_in_keeps_four_tensors_where_it_does_not_apply():
+    """The opt-in saves the reference's four tensors when vals needs no
+    gradient or D > 1."""
+    announce("spmv autograd opt-in outside D=1 with vals grad")
+    from cases.spmv import op
+    ptr, col, vals, X = _csr(np.random.default_rng(2).integers(0, 20, 300), 200, 1, 3)
+    Xd = X.cuda().requires_grad_(True)
+    y = op.candidate({"row_ptr": ptr.cuda(), "col_idx": col.cuda(), "vals": vals.cuda(), "X": Xd},
+                     {"keep_gather": True})
+    assert len(y.grad_fn.saved_tensors) == 4
+    ptr, col, vals, X = _csr(np.random.default_rng(2).integers(0, 20, 300), 200, 8, 3)
+    y = op.candidate({"row_ptr": ptr.cuda(), "col_idx": col.cuda(),
+                      "vals": vals.cuda().requires_grad_(True), "X": X.cuda()},
+                     {"keep_gather": True})
+    assert len(y.grad_fn.saved_tensors) == 4
+
+
+@pytest.mark.parametrize("idx", [torch.int32, torch.int64])
+def test_spmv_malformed_structure_raises_under_check(idx, monkeypatch):
+    """NL2K_CHECK=1 (set for every test here): the device-side structure
+    check raises before any product kernel runs: IndexError for a column
+    outside [0, K), as the reference path's X.index_select(0, col_idx) does
+    (cases/spmv/reference.py:19), RuntimeError for a bad row_ptr.  Without
+    NL2K_CHECK the kernels clamp the index into range (no error, no fault)."""
+    announce(f"spmv structure check ({idx})")
+    from cases.spmv import op
+    ptr, col, vals, X = _csr([3, 0, 2, 4], 10, 1, 5, index_dtype=idx)
+    dY = torch.ones(4, 1, device="cuda")
+    for bad, what in ((10, "= 10 is not in"), (-1, "= -1 is not in")):
+        c = col.clone()
+        c[5] = bad
+        with pytest.raises(IndexError, match=f"col_idx\\[5\\] {what}"):
+            op.spmv_forward(ptr.cuda(), c.cuda(), vals.cuda(), X.cuda())
+        with pytest.raises(IndexError, match="index out of range"):
+            op.spmv_backward(ptr.cuda(), c.cuda(), vals.cuda(), X.cuda(), dY)
+        Xd = X.cuda().requires_grad_(True)
+        with pytest.raises(IndexError):
+            op.candidate({"row_ptr": ptr.cuda(), "col_idx": c.cuda(), "vals": vals.cuda(),
+                          "X": Xd}, {})
+    for r, v, what in ((0, 1, "row_ptr\\[0\\] != 0"), (2, 1, "decreases"),
+                       (4, 8, "row_ptr\\[M\\] != nnz")):
+        p = ptr.clone()
+        p[r] = v
+        with pytest.raises(RuntimeError, match=what):
+            op.spmv_forward(p.cuda(), col.cuda(), vals.cuda(), X.cuda())
+    op.spmv_forward(ptr.cuda(), col.cuda(), vals.cuda(), X.cuda())  # well formed: no error
+    monkeypatch.delenv("NL2K_CHECK")
+    c = col.clone()
+    c[5] = 10
+    y = op.spmv_forward(ptr.cuda(), c.cuda(), vals.cuda(), X.cuda())
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all()
 
 
 def test_spmv_gathered_misaligned():

@@ -1,7 +1,13 @@
 """The case runner CLI (framework/run_case.py): the no-GPU refusal on the
-CPU, and on the GPU the verify-gated bench at a small cosine_sim size with
-the eager baseline, which must print the parity report and one VERDICT line
-in the reference's grammar (skill/scripts/bench_case.py:33-54)."""
+CPU; on the GPU the verify-gated bench at a small cosine_sim size with the
+eager baseline, which must print the parity report and one VERDICT line in
+the reference's grammar (skill/scripts/bench_case.py:33-54), and the
+reference's own headline measurement: ``run_case run --case rbf`` at the
+reference defaults (RBF_SIZE = 2048, D = 64, gamma = 1/64, X, Y ~ N(0,1)),
+parity first, then the candidate against ``torch.compile(reference_forward)``
+(the reference's default baseline, framework/bench.py:129-178) with the
+VERDICT line the reference publishes against (fwd 1.10x / bwd 1.17x on
+A100, cases/rbf/delivery/README.md:56-57)."""
 
 import re
 
@@ -39,3 +45,22 @@ def test_run_gates_bench_on_verify(capsys, monkeypatch):
     assert "=== overall: PASS ===" in out
     assert re.search(r"^VERDICT=(PASS|BENCH_FAIL|CV_INVALID) fwd=[0-9.]+x bwd=[0-9.]+x cv_ok=[01]$",
                      out, re.M)
+
+
+@pytest.mark.gpu
+@pytest.mark.timeout(900)
+def test_rbf_reference_verdict_against_torch_compile(capsys):
+    from conftest import announce
+    from cases.rbf import config
+    announce(f"run_case run --case rbf --emit-verdict (N=M={config.N}, torch.compile baseline)")
+    assert config.N == config.M == 2048 and config.D == 64
+    rc = run_case.main(["run", "--case", "rbf", "--emit-verdict"])
+    out = capsys.readouterr().out
+    print(out)
+    assert rc == 0
+    assert "=== overall: PASS ===" in out
+    assert "[baseline(torch.compile)]" in out
+    m = re.search(r"^VERDICT=(PASS|BENCH_FAIL|CV_INVALID) fwd=([0-9.]+)x bwd=([0-9.]+)x "
+                  r"cv_ok=([01])$", out, re.M)
+    assert m, "no VERDICT line"
+    print(f"[verdict] {m.group(0)}", flush=True)
