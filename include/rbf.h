@@ -67,11 +67,13 @@ int rbf_backward_f32(const float* X, const float* Y, const float* dK,
  * GPU, held from the first call on that GPU until the process ends).  No
  * counterpart in the reference: it is for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc).  Shapes whose
+ * harnesses that forbid hipMalloc).  Calls that take the tile kernels
+ * (D = 64, 16-byte aligned X, Y, dX, dY) and whose
  * rbf_backward_workspace_bytes(N, M, D) exceeds
  * rbf_backward_noalloc_max_bytes() are rejected with NL2K_ERR_WORKSPACE
  * before any HIP call (N = M = 4096, D = 64 needs 34 MB and fits; 8192 does
- * not).  Every call on one GPU shares that GPU's scratch, so calls that
+ * not); calls that take the generic kernels use no scratch and run at any
+ * size.  Every call on one GPU shares that GPU's scratch, so calls that
  * overlap in time on one GPU (different streams, or threads) race and must
  * be serialised by the caller; a call needs no initial scratch contents.
  */

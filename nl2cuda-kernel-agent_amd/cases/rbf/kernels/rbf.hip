@@ -189,6 +189,14 @@ int launch_fill_zero(float* p, size_t count, hipStream_t stream) {
   return nl2k::check_launch("rbf fill");
 }
 
+// The backward's tile kernels (which need the workspace) run for D == 64 and
+// 16-byte aligned X, Y, dX and dY; everything else takes the generic kernels.
+bool takes_tile_path(const nl2k::pairwise::BwdPlan& p, const float* X, const float* Y,
+                     const float* dX, const float* dY) {
+  return p.fast && nl2k::aligned16(X) && nl2k::aligned16(Y) && nl2k::aligned16(dX) &&
+         nl2k::aligned16(dY);
+}
+
 // Both backward entry points: the caller's workspace, or the scratch array
 // below for rbf_backward_f32_noalloc.
 int backward_impl(const float* X, const float* Y, const float* dK, const float* K, float* dX,
@@ -206,9 +214,7 @@ int backward_impl(const float* X, const float* Y, const float* dK, const float* 
 
   const float neg2g = -2.f * gamma;
   const nl2k::pairwise::BwdPlan p = nl2k::pairwise::plan_backward(N, M, D, true);
-  const bool aligned = nl2k::aligned16(X) && nl2k::aligned16(Y) &&
-                       nl2k::aligned16(dX) && nl2k::aligned16(dY);
-  if (p.fast && aligned) {
+  if (takes_tile_path(p, X, Y, dX, dY)) {
     const size_t need = p.ws_floats * sizeof(float);
     if (workspace == nullptr || workspace_bytes < need)
       return nl2k::fail(NL2K_ERR_WORKSPACE, "%s: workspace of %zu bytes required, got %zu", who,
@@ -328,7 +334,10 @@ int rbf_backward_f32_noalloc(const float* X, const float* Y, const float* dK, co
   const char* who = "rbf_backward_f32_noalloc";
   int st = validate_sizes(N, M, D);
   if (st) return st;
-  const size_t need = nl2k::pairwise::plan_backward(N, M, D, true).ws_floats * sizeof(float);
+  // Only the tile path uses scratch; shapes and alignments that take the
+  // generic kernels run whatever their size.
+  const nl2k::pairwise::BwdPlan p = nl2k::pairwise::plan_backward(N, M, D, true);
+  const size_t need = takes_tile_path(p, X, Y, dX, dY) ? p.ws_floats * sizeof(float) : 0;
   if (need > kScratchBytes)
     return nl2k::fail(NL2K_ERR_WORKSPACE,
                       "%s: N=%lld M=%lld D=%lld needs %zu bytes of scratch; the library's static "

@@ -57,7 +57,14 @@ _WORKSPACES = {}
 
 def _workspace(device, stream, nbytes):
     """The workspace kept for (device, stream), allocated only when a larger
-    one is needed (the kernels need no initial contents)."""
+    one is needed (the kernels need no initial contents).  While the stream
+    is being captured into a graph every call gets a fresh workspace, which
+    the graph's memory pool then owns: a graph keeps the address it was
+    captured with, so it must not share one that a later eager call could
+    replace and free, nor one with another graph captured on the same
+    (shared capture) stream."""
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty(max((nbytes + 7) // 8, 1), dtype=torch.int64, device=device)
     key = (device.index, stream.value)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() * 8 < nbytes:

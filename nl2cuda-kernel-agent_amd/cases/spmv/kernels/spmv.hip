@@ -858,24 +858,32 @@ __global__ __launch_bounds__(kThreads) void spmm_bwd_kernel(
 // dX = A^T dY without atomics and bitwise repeatable: a stable column-major
 // copy of A is built in the workspace (its entries of column c in
 // increasing position order), then each column gathers dY rows in that
-// order.  Positions are cut into chunks of P (whole rows: chunk w takes the
-// rows that start in [wP, (w+1)P)), one wave each.
-//  S1 spmm_t_hist_kernel:    H[w][c] = entries of column c in chunk w
-//                            (an LDS histogram, order-free integer counts).
-//  S2 spmm_t_offsets_kernel: 256 columns per workgroup; column totals, the
-//                            exclusive scan over columns (block prefix plus
-//                            the earlier blocks' totals, passed through
-//                            nonce-tagged slots and added in block order),
-//                            colptr, and H rewritten in place as each
-//                            chunk's first slot per column.
-//  S3 spmm_t_scatter_kernel: each chunk walks its rows in order and places
-//                            every entry at its column's LDS cursor, so
-//                            entries of one column land in position order
-//                            (within one 64-position step of a row, lanes
-//                            that share a column, found through LDS tags,
-//                            take slots in lane order), as one 16-byte
-//                            record {row, position, value} per entry.
-//  S4 spmm_t_gather_kernel:  L lanes per column sum vals * dY[row] over the
+// order.  Positions are cut into chunks of P (P >= 1024, a multiple of 256,
+// about one chunk per CU): chunk w = positions [wP, (w+1)P), one workgroup
+// per chunk in S1 and S3.
+//  S1 spmm_t_hist_kernel:    H[w][c] = entries of column c in chunk w, an LDS
+//                            histogram (order-free integer counts), eight
+//                            column loads per thread in flight.
+//  S2 spmm_t_offsets_kernel: kOffCols = 16 columns per workgroup, the chunks
+//                            split over 16 thread groups (each holds up to 16
+//                            chunks' counts in registers); column totals,
+//                            the exclusive scan over columns (this block's
+//                            prefix plus the earlier blocks' totals, passed
+//                            through nonce-tagged slots, 256 slots loaded
+//                            per round trip), colptr, and H rewritten in
+//                            place as each chunk's first slot per column.
+//  S3 spmm_t_scatter_kernel: each chunk finds every position's row (an LDS
+//                            copy of the chunk's row starts, else a binary
+//                            search) and walks its positions in 256-position
+//                            tiles, kScatterTiles tiles' loads in flight per
+//                            pass; within a tile the four waves take their
+//                            slots one after another, and lanes of a wave
+//                            that share a column (found through LDS tags)
+//                            take consecutive slots in lane order, so the
+//                            entries of every column land in position order,
+//                            as one 16-byte record {row, position, value}.
+//  S4 spmm_t_gather_kernel:  L lanes per column (G groups of them share a
+//                            long column) sum vals * dY[row] over the
 //                            column's entries in that order, 16 entries per
 //                            step (and, when asked and D fits one pass,
 //                            dvals[p] = dY[row] . X[c]).
@@ -1844,14 +1852,8 @@ int transpose_backward(const TransposePlan& tp, const I* ptr, const I* col, cons
   const size_t lds = (size_t)K * sizeof(int);               // histogram kernel
   const size_t lds_s = lds + (size_t)nl2k::ceil_div(K, 4) * 4;  // cursors + tags
   if (lds_s > (48u << 10)) {  // up to 80 KB of dynamic LDS (K <= 16384)
-    st = nl2k::check_hip(hipFuncSetAttribute((const void*)&spmm_t_hist_kernel<I>,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
-                         "hipFuncSetAttribute");
-    if (!st)
-      st = nl2k::check_hip(hipFuncSetAttribute((const void*)&spmm_t_scatter_kernel<I>,
-                                               hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               (int)lds_s),
-                           "hipFuncSetAttribute");
+    st = nl2k::raise_dynamic_lds((const void*)&spmm_t_hist_kernel<I>, (int)lds);
+    if (!st) st = nl2k::raise_dynamic_lds((const void*)&spmm_t_scatter_kernel<I>, (int)lds_s);
     if (st) return st;
   }
   hipLaunchKernelGGL((spmm_t_hist_kernel<I>), dim3((unsigned)tp.n_chunks), dim3(kThreads), lds,

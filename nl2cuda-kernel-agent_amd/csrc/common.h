@@ -71,6 +71,24 @@ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // the runtime computes from the kernel's registers, LDS and launch bounds.
 // Cached per (device, kernel), so instantiations with equal signatures but
 // different register counts keep their own figures.
+// Raises `kernel`'s dynamic LDS limit to at least `bytes` on the current
+// device.  The attribute call is made once per (device, kernel) and size
+// increase; later calls, captured into a graph or not, make none.
+inline int raise_dynamic_lds(const void* kernel, int bytes) {
+  static std::mutex mu;
+  static std::map<std::pair<int, const void*>, int> set;
+  int dev = 0;
+  int st = check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (st) return st;
+  std::lock_guard<std::mutex> lock(mu);
+  int& have = set[{dev, kernel}];
+  if (bytes <= have) return NL2K_SUCCESS;
+  st = check_hip(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes),
+                 "hipFuncSetAttribute(MaxDynamicSharedMemorySize)");
+  if (!st) have = bytes;
+  return st;
+}
+
 inline int resident_blocks(const void* kernel, int threads, int* out) {
   static std::mutex mu;
   static std::map<std::pair<int, const void*>, int> cache;

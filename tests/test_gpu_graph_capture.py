@@ -56,6 +56,35 @@ def test_scan_graph_replays_with_new_inputs(rows, d):
         assert torch.equal(eager, y_static), f"replay {seed} differs from the eager call"
 
 
+def test_scan_graphs_keep_their_own_workspaces():
+    """Two graphs, each holding a multi-chunk scan, captured on the shared
+    capture stream, replayed alternately with a larger eager scan between
+    the replays (which replaces the eagerly cached workspace): every replay
+    still matches the oracle."""
+    announce("scan: two captured graphs and eager calls in between")
+    from cases.scan import op
+    xa = torch.zeros(8, 40000, device="cuda")
+    xb = torch.zeros(5, 70001, device="cuda")
+    ga, ya = _capture(lambda: op.scan_forward(xa))
+    gb, yb = _capture(lambda: op.scan_forward(xb))
+    for seed in range(3):
+        gen = torch.Generator().manual_seed(300 + seed)
+        a = (torch.rand(8, 40000, generator=gen, dtype=torch.float64) * 2 - 1).float()
+        b = (torch.rand(5, 70001, generator=gen, dtype=torch.float64) * 2 - 1).float()
+        xa.copy_(a.cuda())
+        xb.copy_(b.cuda())
+        ga.replay()
+        gb.replay()
+        big = op.scan_forward(torch.ones(16 + seed, 300000, device="cuda"))
+        torch.cuda.synchronize()
+        assert float(big[0, -1]) == 300000.0
+        for name, y, x in (("a", ya, a), ("b", yb, b)):
+            ref = oscan.cumsum_f32(x.numpy()).astype(np.float64)
+            err = np.abs(y.cpu().numpy().astype(np.float64) - ref)
+            print(f"  replay {seed} graph {name}: max_abs={err.max():.3e}")
+            assert np.all(err <= 1e-3 + 1e-3 * np.abs(ref)), f"replay {seed} graph {name}"
+
+
 def test_scan_int_graph_replays_bit_exact():
     announce("scan int32 -> int64 graph capture [64, 65536]")
     from cases.scan import op
@@ -95,11 +124,24 @@ def test_softmax_ce_forward_graph_replays_with_new_inputs():
         assert torch.equal(eager, loss_static), f"replay {seed} differs from the eager call"
 
 
-def test_spmm_backward_graph_replays_with_new_inputs():
-    announce("spmm backward graph capture (reference default M=K=4096 D=64)")
+def _wide_spmm_inputs(m=2048, k=16384, d=8, per_row=64, seed=0):
+    """M x K CSR with per_row sorted unique random columns per row, X [K, D]."""
+    rng = np.random.default_rng(seed)
+    cols = np.sort(np.stack([rng.choice(k, per_row, replace=False) for _ in range(m)]), axis=1)
+    ptr = np.arange(m + 1, dtype=np.int64) * per_row
+    g = torch.Generator().manual_seed(seed)
+    return {"row_ptr": torch.from_numpy(ptr), "col_idx": torch.from_numpy(cols.reshape(-1)),
+            "vals": torch.randn(m * per_row, generator=g), "X": torch.randn(k, d, generator=g)}
+
+
+@pytest.mark.parametrize("shape", ["reference default M=K=4096 D=64",
+                                   "K=16384 D=8 (80 KB of scatter LDS)"])
+def test_spmm_backward_graph_replays_with_new_inputs(shape):
+    announce(f"spmm backward graph capture ({shape})")
     from cases.spmv import op, reference as ref
     from oracle import spmv as osp
-    t = ref.make_inputs(0, torch.float32, "cpu")
+    t = ref.make_inputs(0, torch.float32, "cpu") if shape.startswith("reference") \
+        else _wide_spmm_inputs()
     ptr, col, vals, X = (t[k].cuda() for k in ("row_ptr", "col_idx", "vals", "X"))
     M, D = ptr.numel() - 1, X.shape[1]
     dy_static = torch.zeros(M, D, device="cuda")

@@ -3,7 +3,8 @@ workspace entry point rbf_backward_f32 through the C-ABI: bit-identical dX
 and dY (same kernels, same order of additions), both within atol = rtol =
 1e-3 of the float64 oracle, on calls in a row whose later shapes are smaller
 (the library's scratch keeps the previous call's partials), on the vector
-and the scalar tile paths, and a shape beyond the scratch rejected."""
+and the scalar tile paths; a tile-path shape beyond the scratch rejected,
+and a generic-path call beyond it run without scratch."""
 
 import numpy as np
 import pytest
@@ -66,3 +67,39 @@ def test_noalloc_backward_rejects_a_shape_beyond_its_scratch():
     st = lib.rbf_backward_f32_noalloc(P(x), P(x), P(x), P(x), P(x), P(x), 8192, 8192, 64, 0.5,
                                       capi.stream_of(x))
     assert st != 0 and b"scratch" in lib.rbf_last_error()
+
+
+def test_noalloc_backward_generic_path_needs_no_scratch():
+    """A misaligned X takes the generic kernels, which use no scratch: the
+    no-alloc entry runs it even where the tile path's partials would not fit
+    (N = M = 6000 needs 75 MB of them), bit-identical to the workspace entry."""
+    n = m = 6000
+    announce(f"rbf noalloc, misaligned X, n={n} m={m} (generic kernels)")
+    from cases.rbf import op
+    lib = op._lib()
+    gamma = 0.5
+    assert lib.rbf_backward_workspace_bytes(n, m, 64) > lib.rbf_backward_noalloc_max_bytes()
+    X, Y, G = _inputs(n, m, 3)
+    buf = torch.empty(n * 64 + 1, device="cuda")
+    Xd = buf[1:].view(n, 64)
+    Xd.copy_(X.cuda())
+    Yd, Gd = Y.cuda(), G.cuda()
+    K = op.rbf_forward(Xd, Yd, gamma)
+    P = capi.ptr
+    dX0, dY0 = torch.empty(n, 64, device="cuda"), torch.empty(m, 64, device="cuda")
+    ws = torch.empty(8, dtype=torch.uint8, device="cuda")
+    st = lib.rbf_backward_f32(P(Xd), P(Yd), P(Gd), P(K), P(dX0), P(dY0), n, m, 64, gamma, P(ws),
+                              0, capi.stream_of(Xd))
+    capi.check(st, lib.rbf_last_error, "rbf_backward_f32 (misaligned X)")
+    dX1, dY1 = torch.empty_like(dX0), torch.empty_like(dY0)
+    st = lib.rbf_backward_f32_noalloc(P(Xd), P(Yd), P(Gd), P(K), P(dX1), P(dY1), n, m, 64, gamma,
+                                      capi.stream_of(Xd))
+    capi.check(st, lib.rbf_last_error, "rbf_backward_f32_noalloc (misaligned X)")
+    torch.cuda.synchronize()
+    assert torch.equal(dX0, dX1) and torch.equal(dY0, dY1)
+    sub = slice(0, 48)  # the oracle on a row block: dX rows need all of Y and G's rows
+    Kr = orbf.forward_f64(X.numpy()[sub], Y.numpy(), gamma)
+    dXr, _ = orbf.backward_f64(X.numpy()[sub], Y.numpy(), G.numpy()[sub], Kr, gamma)
+    err = np.abs(dX1[sub].cpu().double().numpy() - dXr)
+    print(f"  dX rows 0-47: max_abs={err.max():.3e}")
+    assert np.all(err <= 1e-3 + 1e-3 * np.abs(dXr))
