@@ -596,7 +596,7 @@ __global__ __launch_bounds__(512) void pair_bwd_d64_kernel(
 // Otherwise every tile is loaded with clamped addresses and masked
 // (float4 loads: the launcher sends scalar-load shapes to
 // pair_bwd_d64_kernel).
-template <class Op, int JC, bool kFull>
+template <class Op, int JC, bool kFull, bool kQX>
 __global__ __launch_bounds__(768) void pair_bwd_d64_3r_kernel(
     const float* X, const float* __restrict__ Y,
     const float* dK, const float* Kf,
@@ -723,6 +723,19 @@ __global__ __launch_bounds__(768) void pair_bwd_d64_3r_kernel(
   // (clamped; at the last chunk that rewrites the chunk in use with
   // identical bits).
   auto x_chunk = [&](int t) { return min(t / n_jc + 1, n_ic - 1); };
+  // kQX (every region four column tiles wide): step t publishes only part
+  // t % 4 (16 of the 64 columns) of that chunk, so the next chunk is
+  // complete after the four steps of the current one, with one X load and
+  // four LDS writes per lane per step instead of four and sixteen.
+  auto load_x_part = [&](int pos, int part, f32x4& xs) {
+    xs = buffer_load4(rxx, xlane_off, (ibase + chunk_at(pos) * kTile) * kD * 4 + 64 * part);
+  };
+  auto commit_x_part = [&](int pos, int part, const f32x4& xs) {
+    float* dst = Xt[pos & 1] + 16 * part * kLds;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) dst[(xcol + u) * kLds + xrow] = xs[u];
+  };
+  f32x4 g_xq;
 
   // Tile 0's loads go out first.  The region's Y rows are staged by waves
   // 0-7 as four 64-column chunks, transposed into Yt[d][j]: the chunk of the
@@ -794,7 +807,8 @@ __global__ __launch_bounds__(768) void pair_bwd_d64_3r_kernel(
     // the loop's first step of every three waited for the previous step's
     // tiles.
     commit_x(0, g_x, g_xs);
-    load_x(x_chunk(0), g_x, g_xs);
+    if constexpr (kQX) load_x_part(x_chunk(0), 0, g_xq);
+    else load_x(x_chunk(0), g_x, g_xs);
     __builtin_amdgcn_sched_barrier(0);
     load_stage(min(1, n_tiles - 1), g_dk[1], g_k[1], g_ok[1]);
     load_stage(min(2, n_tiles - 1), g_dk[2], g_k[2], g_ok[2]);
@@ -804,8 +818,13 @@ __global__ __launch_bounds__(768) void pair_bwd_d64_3r_kernel(
     auto step = [&](int t, f32x4 (&ldk)[4], f32x4 (&lk)[4], bool (&lok)[4],
                     const f32x4 (&cdk)[4], const f32x4 (&ck)[4], const bool (&cok)[4]) {
       __builtin_amdgcn_sched_barrier(0);
-      commit_x(x_chunk(t), g_x, g_xs);
-      load_x(x_chunk(t + 1), g_x, g_xs);
+      if constexpr (kQX) {
+        commit_x_part(x_chunk(t), t & 3, g_xq);
+        load_x_part(x_chunk(t + 1), (t + 1) & 3, g_xq);
+      } else {
+        commit_x(x_chunk(t), g_x, g_xs);
+        load_x(x_chunk(t + 1), g_x, g_xs);
+      }
       load_stage(min(t + 3, n_tiles - 1), ldk, lk, lok);
       commit_stage(t + 1, cdk, ck, cok);
       __builtin_amdgcn_sched_barrier(0);
@@ -1003,12 +1022,18 @@ void launch_bwd_tiles(const BwdPlan& p, const float* X, const float* Y, const fl
   // staging needs the registers the third role takes).
   const bool full = N % kTile == 0 && M % kTile == 0 &&
                     (int64_t)N * M * (int64_t)sizeof(float) < ((int64_t)1 << 31);
-  if (vec_nm && full)
-    hipLaunchKernelGGL((pair_bwd_d64_3r_kernel<Op, JC, true>), dim3(p.nRI * p.nRJ), dim3(768),
-                       0, stream, X, Y, dK, K, Px, Rx, Py, Ry, N, M, p.R, p.nRJ, sx, sy);
+  // Quarter X publishing needs four column tiles in every region.
+  const bool qx = full && JC == 4 && M % (4 * kTile) == 0 && !Op::kScale;
+  if (vec_nm && qx)
+    hipLaunchKernelGGL((pair_bwd_d64_3r_kernel<Op, JC, true, JC == 4 && !Op::kScale>),
+                       dim3(p.nRI * p.nRJ), dim3(768), 0, stream, X, Y, dK, K, Px, Rx, Py, Ry, N, M,
+                       p.R, p.nRJ, sx, sy);
+  else if (vec_nm && full)
+    hipLaunchKernelGGL((pair_bwd_d64_3r_kernel<Op, JC, true, false>), dim3(p.nRI * p.nRJ),
+                       dim3(768), 0, stream, X, Y, dK, K, Px, Rx, Py, Ry, N, M, p.R, p.nRJ, sx, sy);
   else if (vec_nm)
-    hipLaunchKernelGGL((pair_bwd_d64_3r_kernel<Op, JC, false>), dim3(p.nRI * p.nRJ), dim3(768),
-                       0, stream, X, Y, dK, K, Px, Rx, Py, Ry, N, M, p.R, p.nRJ, sx, sy);
+    hipLaunchKernelGGL((pair_bwd_d64_3r_kernel<Op, JC, false, false>), dim3(p.nRI * p.nRJ),
+                       dim3(768), 0, stream, X, Y, dK, K, Px, Rx, Py, Ry, N, M, p.R, p.nRJ, sx, sy);
   else
     hipLaunchKernelGGL((pair_bwd_d64_kernel<Op, JC, false>), dim3(p.nRI * p.nRJ), dim3(512), 0,
                        stream, X, Y, dK, K, Px, Rx, Py, Ry, N, M, p.R, p.nRJ, sx, sy);
