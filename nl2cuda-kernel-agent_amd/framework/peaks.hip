@@ -87,6 +87,92 @@ __global__ __launch_bounds__(kBlock) void peak_mfma_f32_kernel(float* __restrict
   }
 }
 
+// Co-execution of memory staging and fp32 MFMA on one CU.  One workgroup
+// of 12 waves per CU (the dynamic LDS allotment keeps it alone there):
+// waves 8-11 ("stagers", one per SIMD) stream `tiles` 64 x 64 fp32 tile
+// pairs of two [kCoN, kCoN] arrays, the pair of region (blockIdx / 16,
+// blockIdx % 16) in the backward's order, 32 KB per CU per tile, each
+// through registers into LDS (direct == 0) or straight into LDS
+// (global_load_lds_dwordx4, direct == 1), waiting for every tile before the
+// next; waves 0-7 (two per SIMD) meanwhile run mfma_iters x 8 independent
+// fp32 MFMAs (kind 1: 16x16x4, kind 2: 32x32x2 as 4 chains x 2) or nothing
+// (kind 0).  ticks[4 b + w] = 100 MHz ticks of stager w of workgroup b,
+// ticks[1024 + 8 b + w] those of MFMA wave w.
+constexpr int kCoN = 4096;
+constexpr int kCoLds = 96 * 1024;
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+__global__ __launch_bounds__(768) void peak_coexec_kernel(
+    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ out,
+    unsigned long long* __restrict__ ticks, int tiles, int kind, int mfma_iters, int direct) {
+  extern __shared__ float co_lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ri = blockIdx.x / 16, rj = blockIdx.x % 16;
+  if (wave < 8) {
+    const unsigned long long m0 = __builtin_amdgcn_s_memrealtime();
+    const float a = 1e-3f * (float)lane, b = 1.0f;
+    float s = 0.f;
+    if (kind == 1) {
+      f32x4 acc[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = nl2k::zero4();
+      for (int i = 0; i < mfma_iters; ++i) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = nl2k::mfma16x4(a, b, acc[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += acc[j][0];
+    } else if (kind == 2) {
+      f32x16 acc[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+      for (int i = 0; i < mfma_iters; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[j], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b, a, acc[j], 0, 0, 0);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s += acc[j][0];
+    }
+    const unsigned long long m1 = __builtin_amdgcn_s_memrealtime();
+    if (lane == 0 && blockIdx.x < 256) ticks[1024 + 8 * blockIdx.x + wave] = m1 - m0;
+    if (s == 1234.5f) out[0] = s;
+    return;
+  }
+  const int w = wave - 8;
+  const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+  for (int it = 0; it < tiles; ++it) {
+    const int t = it % 16, ic = t / 4, jc = t % 4;
+    const int row0 = ri * 256 + ic * 64 + w * 16 + (lane >> 4);
+    const int col = rj * 256 + jc * 64 + (lane & 15) * 4;
+    float* st = co_lds + (it & 1) * 8192 + w * 2048;
+    if (direct) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        __builtin_amdgcn_global_load_lds(A + (size_t)(row0 + 4 * s) * kCoN + col, st + s * 256, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(B + (size_t)(row0 + 4 * s) * kCoN + col, st + (4 + s) * 256, 16, 0, 0);
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else {
+      f32x4 v[8];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        v[s] = *reinterpret_cast<const f32x4*>(A + (size_t)(row0 + 4 * s) * kCoN + col);
+        v[4 + s] = *reinterpret_cast<const f32x4*>(B + (size_t)(row0 + 4 * s) * kCoN + col);
+      }
+#pragma unroll
+      for (int s = 0; s < 8; ++s) *reinterpret_cast<f32x4*>(st + s * 256 + lane * 4) = v[s];
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+  }
+  const unsigned long long t1 = __builtin_amdgcn_s_memrealtime();
+  if (lane == 0 && blockIdx.x < 256) ticks[4 * blockIdx.x + w] = t1 - t0;
+  if (co_lds[lane] == 1234.5f) out[1] = co_lds[lane + 64];
+}
+
 bool bad_stream_args(int64_t n4, int blocks) { return n4 < 1 || blocks < 1 || blocks > (1 << 20); }
 
 }  // namespace
@@ -137,6 +223,20 @@ int peaks_mfma_f32(float* out, unsigned long long* clk, int blocks, int iters,
     return nl2k::fail(NL2K_ERR_SHAPE, "peaks_mfma_f32: bad arguments");
   hipLaunchKernelGGL(peak_mfma_f32_kernel, dim3(blocks), dim3(kBlock), 0, stream, out, clk, iters);
   return nl2k::check_launch("peaks_mfma_f32");
+}
+
+// Co-execution probe (peak_coexec_kernel): A and B are [4096, 4096] fp32,
+// out holds 2 floats, ticks 3072 values; blocks <= 256 (one per CU).
+int peaks_coexec(const float* A, const float* B, float* out, unsigned long long* ticks, int blocks,
+                 int tiles, int kind, int mfma_iters, int direct, hipStream_t stream) {
+  if (!A || !B || !out || !ticks || blocks < 1 || blocks > 256 || tiles < 1 || kind < 0 ||
+      kind > 2 || mfma_iters < 0 || (direct != 0 && direct != 1))
+    return nl2k::fail(NL2K_ERR_SHAPE, "peaks_coexec: bad arguments");
+  int st = nl2k::raise_dynamic_lds((const void*)&peak_coexec_kernel, kCoLds);
+  if (st) return st;
+  hipLaunchKernelGGL(peak_coexec_kernel, dim3(blocks), dim3(768), kCoLds, stream, A, B, out, ticks,
+                     tiles, kind, mfma_iters, direct);
+  return nl2k::check_launch("peaks_coexec");
 }
 
 }  // extern "C"

@@ -29,7 +29,13 @@ copy rate there is the practical ceiling of a kernel that reads and writes
 that many bytes once.  Run it under rocprofv3 --kernel-trace --stats for the
 kernel-time figures beside the event times printed here.
 
+--coexec instead measures memory staging beside fp32 MFMA work on every CU
+(peak_coexec_kernel): four staging waves stream 64 x 64 tile pairs (the RBF
+backward's pattern) while eight waves run MFMAs, which shows how much of
+the memory side an MFMA-bound kernel can keep going on waves of its own.
+
 Usage:  python nl2cuda-kernel-agent_amd/framework/peaks.py [--iters 20]
+        python nl2cuda-kernel-agent_amd/framework/peaks.py --coexec
         python nl2cuda-kernel-agent_amd/framework/peaks.py --sized-copy 16,64,128
 """
 
@@ -64,6 +70,7 @@ def bind_library(lib):
     capi.bind(lib, "peaks_copy_f32x4", [V, V, I64, I, V])
     capi.bind(lib, "peaks_mfma_f32_flops", [I, I], capi.c_double)
     capi.bind(lib, "peaks_mfma_f32", [V, V, I, I, V])
+    capi.bind(lib, "peaks_coexec", [V, V, V, V, I, I, I, I, I, V])
     capi.bind_last_error(lib, "peaks_last_error")
     return lib
 
@@ -151,6 +158,54 @@ def sized_copy(sizes_mib, iters, blocks=None):
     return 0
 
 
+def coexec(iters, tiles=64, mfma_iters=3840):
+    """Staging waves beside fp32 MFMA waves on every CU (peak_coexec_kernel):
+    the stagers' time per 32 KB tile pair and the MFMA waves' rate, for no
+    MFMA, 16x16x4 and 32x32x2 MFMAs, staging through registers or straight
+    into LDS.  Prints one JSON line per configuration and a table."""
+    import torch
+    dev = torch.device("cuda:0")
+    lib = _lib()
+    s = capi.stream_of(torch.empty(1, device=dev))
+    P = capi.ptr
+    n = 4096
+    A = torch.ones(n * n, device=dev)
+    B = torch.ones(n * n, device=dev)
+    out = torch.zeros(2, device=dev)
+    ticks = torch.zeros(3072, dtype=torch.int64, device=dev)
+    blocks = min(256, torch.cuda.get_device_properties(dev).multi_processor_count)
+    flops_per = {1: 2.0 * 16 * 16 * 4, 2: 2.0 * 32 * 32 * 2}
+    names = {0: "none", 1: "16x16x4", 2: "32x32x2"}
+    rows = []
+    for kind in (0, 1, 2):
+        for direct in (0, 1):
+            tile_ns, mfma_tf = [], []
+            for _ in range(iters):
+                capi.check(lib.peaks_coexec(P(A), P(B), P(out), P(ticks), blocks, tiles, kind,
+                                            mfma_iters, direct, s), lib.peaks_last_error, "peaks")
+                torch.cuda.synchronize()
+                t = ticks.cpu().numpy()
+                tile_ns.append(statistics.median(t[:4 * blocks].tolist()) * 10.0 / tiles)
+                if kind:
+                    mt = statistics.median(t[1024:1024 + 8 * blocks].tolist()) * 10.0
+                    mfma_tf.append(blocks * 8 * mfma_iters * 8 * flops_per[kind] / (mt * 1e-9) / 1e12)
+            ns = statistics.median(tile_ns)
+            tf = statistics.median(mfma_tf) if mfma_tf else None
+            row = {"rate": "staging beside MFMA", "mfma": names[kind],
+                   "staging": "direct to LDS" if direct else "through registers",
+                   "ns_per_tile": round(ns, 1), "staging_tbs": round(blocks * 32768 / ns / 1e3, 2),
+                   "mfma_tflops": round(tf, 1) if tf else None}
+            print(json.dumps(row), flush=True)
+            rows.append(row)
+    print("\n| MFMA waves (2 per SIMD) | staging | ns per 32 KB tile pair per CU | staging TB/s "
+          "(chip) | MFMA TFLOP/s |")
+    print("|---|---|---:|---:|---:|")
+    for r in rows:
+        print(f"| {r['mfma']} | {r['staging']} | {r['ns_per_tile']:,.0f} | {r['staging_tbs']:.2f} | "
+              f"{r['mfma_tflops'] if r['mfma_tflops'] else '-'} |")
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--iters", type=int, default=20)
@@ -159,11 +214,15 @@ def main(argv=None):
                     help="comma-separated MiB: copy at these sizes (flushed) instead")
     ap.add_argument("--blocks", default=None,
                     help="comma-separated workgroup counts for --sized-copy (default: a sweep)")
+    ap.add_argument("--coexec", action="store_true",
+                    help="staging waves beside MFMA waves on one CU instead (peak_coexec_kernel)")
     ns = ap.parse_args(argv)
     import torch
     if not torch.cuda.is_available():
         print("peaks: needs the GPU", file=sys.stderr)
         return 2
+    if ns.coexec:
+        return coexec(min(ns.iters, 7))
     if ns.sized_copy:
         blocks = tuple(int(v) for v in ns.blocks.split(",")) if ns.blocks else None
         return sized_copy([int(v) for v in ns.sized_copy.split(",")], ns.iters, blocks)

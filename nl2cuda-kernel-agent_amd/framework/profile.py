@@ -22,6 +22,10 @@ commit next to the code:
            MFMA pipes' busy cycles over all SIMDs and the GPU-active
            cycles) and MfmaFlopsF32 (fp32 MFMA flops) for the selected
            kernels, per dispatch.  Writes <out>/<name>_mfma.json and .md.
+  gaps     rocprofv3 --kernel-trace over a command; for a repeated sequence
+           of dispatches (kernel-name substrings, --sequence "a;b;c") the
+           median duration of each and the gap between consecutive ones
+           (start minus the previous end).  Writes <out>/<name>.md.
   run-case the profiled program for a case: warmup, then --iters steps of
            the case's candidate (forward only or forward+backward).
 
@@ -122,6 +126,67 @@ def cmd_stats(ns, cmd):
     with open(path, "w") as f:
         f.write("\n".join(lines) + "\n")
     print("\n".join(lines[-len(table) - 2:]))
+    print(f"[profile] wrote {path}")
+    return 0
+
+
+def trace_rows(d):
+    """(start ns, end ns, kernel name) of every dispatch, in start order."""
+    with open(_find(d, "kernel_trace.csv")) as f:
+        rows = [(int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"])
+                for r in csv.DictReader(f)]
+    return sorted(rows)
+
+
+def sequence_gaps(rows, pattern):
+    """Every run of consecutive dispatches whose names contain pattern[0],
+    pattern[1], ... in order.  Returns {"dur <k>": [us], "gap <k-1> -> <k>":
+    [us]} over the runs: each element's duration and the idle time between
+    the end of one element and the start of the next (negative when the next
+    dispatch's start was stamped before the previous one ended)."""
+    out = {}
+    for i in range(len(rows) - len(pattern) + 1):
+        run = rows[i:i + len(pattern)]
+        if not all(p in r[2] for p, r in zip(pattern, run)):
+            continue
+        for k, (p, r) in enumerate(zip(pattern, run)):
+            out.setdefault(f"dur {p}", []).append((r[1] - r[0]) / 1e3)
+            if k:
+                out.setdefault(f"gap {pattern[k - 1]} -> {p}", []).append(
+                    (r[0] - run[k - 1][1]) / 1e3)
+    return out
+
+
+def cmd_gaps(ns, cmd):
+    """Kernel durations and the gaps between them for a repeated sequence of
+    dispatches (one rocprofv3 --kernel-trace pass)."""
+    d = _rocprof(["--kernel-trace", "--stats"], ns.raw, f"{ns.name}_trace", cmd, ns.limit)
+    rows = trace_rows(d)
+    lines = [f"# rocprofv3 kernel trace, durations and gaps: {ns.name}", "",
+             "Command (repository root, `cd` into it first; TMPDIR=/tmp):", "",
+             "```", " ".join(shlex.quote(c) for c in _INVOCATION), "```", "",
+             "which ran:", "", "```",
+             "rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o run -- " +
+             " ".join(shlex.quote(c) for c in cmd), "```", "",
+             "A gap is the start of a dispatch minus the end of the one before it, from the "
+             "trace's own timestamps."]
+    for seq in ns.sequence.split("|"):
+        pattern = [p for p in seq.split(";") if p]
+        res = sequence_gaps(rows, pattern)
+        if not res:
+            raise RuntimeError(f"no run of {pattern} in the trace")
+        n = len(next(iter(res.values())))
+        lines += ["", f"Sequence (kernel-name substrings, in dispatch order): "
+                      f"`{' ; '.join(pattern)}`, {n} occurrences.", "",
+                  "| interval | median µs | min µs | max µs |", "|---|---:|---:|---:|"]
+        for k, v in res.items():
+            v = sorted(v)
+            lines.append(f"| {k} | {v[len(v) // 2]:.2f} | {v[0]:.2f} | {v[-1]:.2f} |")
+    os.makedirs(ns.out, exist_ok=True)
+    path = os.path.join(ns.out, f"{ns.name}.md")
+    with open(path, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines[14:]))
     print(f"[profile] wrote {path}")
     return 0
 
@@ -384,7 +449,7 @@ def main(argv=None):
         argv, cmd = argv[:k], argv[k + 1:]
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     sub = ap.add_subparsers(dest="what", required=True)
-    for name in ("stats", "traffic", "mfma", "counters"):
+    for name in ("stats", "traffic", "mfma", "counters", "gaps"):
         p = sub.add_parser(name)
         p.add_argument("--name", required=True)
         p.add_argument("--out", default=os.path.join(REPO, "profiles"))
@@ -399,6 +464,10 @@ def main(argv=None):
         if name in ("traffic", "mfma", "counters"):
             p.add_argument("--kernels", required=True,
                            help="kernel-name substrings, ','-separated (';' when names hold commas)")
+        if name == "gaps":
+            p.add_argument("--sequence", required=True,
+                           help="kernel-name substrings of a repeated sequence, ';'-separated; "
+                                "several sequences '|'-separated")
         if name == "traffic":
             p.add_argument("--algorithmic-bytes", type=int, default=0,
                            help="algorithmic bytes per launch of the listed kernels (for the ratio)")
@@ -416,7 +485,7 @@ def main(argv=None):
     if not cmd:
         ap.error("give a command after -- or --case")
     return {"stats": cmd_stats, "traffic": cmd_traffic, "mfma": cmd_mfma,
-            "counters": cmd_counters}[ns.what](ns, cmd)
+            "counters": cmd_counters, "gaps": cmd_gaps}[ns.what](ns, cmd)
 
 
 if __name__ == "__main__":

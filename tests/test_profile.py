@@ -132,3 +132,19 @@ def test_counter_summary_medians_and_missing_counters():
     assert s["pair_bwd"]["TCC_HIT_sum"]["median"] == 7.0
     assert "TCC_MISS_sum" not in s["pair_bwd"]
     assert s["rbf_bwd_reduce"] == {"TCC_REQ_sum": {"dispatches": 1, "median": 2.0}}
+
+
+def test_sequence_gaps_pairs_durations_and_gaps():
+    from framework.profile import sequence_gaps
+    rows = [(0, 100_000, "reduce_kernel<512"), (105_000, 135_000, "pair_fwd_d64"),
+            (140_000, 190_000, "pair_bwd_d64_3r"), (190_000, 197_000, "rbf_bwd_reduce"),
+            (300_000, 400_000, "reduce_kernel<512"), (406_000, 437_000, "pair_fwd_d64"),
+            (443_000, 492_000, "pair_bwd_d64_3r"), (492_500, 499_000, "rbf_bwd_reduce"),
+            (600_000, 700_000, "other")]
+    g = sequence_gaps(rows, ["reduce_kernel<512", "pair_fwd", "pair_bwd", "rbf_bwd_reduce"])
+    assert g["dur pair_fwd"] == [30.0, 31.0]
+    assert g["gap reduce_kernel<512 -> pair_fwd"] == [5.0, 6.0]
+    assert g["gap pair_fwd -> pair_bwd"] == [5.0, 6.0]
+    assert g["gap pair_bwd -> rbf_bwd_reduce"] == [0.0, 0.5]
+    assert g["dur rbf_bwd_reduce"] == [7.0, 6.5]
+    assert sequence_gaps(rows, ["pair_bwd", "pair_fwd"]) == {}
