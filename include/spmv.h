@@ -20,11 +20,14 @@
  * dvals are deterministic; the D == 1 forward's order of additions does not
  * depend on how rows are split between waves (which follows the device's CU
  * count), so it gives the same bits on any device.  At D > 1 with K <= 16384 (the reference's
- * default SpMM: M = K = 4096, D = 64) dX is deterministic too: a stable
- * column-major copy of A is built in the workspace and each dX row is
- * summed over its column's entries in position order.  At D == 1, and at
- * D > 1 beyond 16384 columns, the order of the additions into each dX
- * element varies between runs (as with the reference's atomics).
+ * default SpMM: M = K = 4096, D = 64) dX is deterministic too: each dX row
+ * is summed over its column's entries in position order, from entries
+ * ordered by column in the workspace (sorted by block of 16 or 64 columns
+ * per 1024-position chunk when D % 4 == 0, D <= 64, K <= 4096 (D > 16) or
+ * 16384 (D <= 16) and X, dY, dX are 16-byte aligned; else a column-major
+ * copy of A).  At D == 1, and at D > 1 beyond 16384 columns, the order of
+ * the additions into each dX element varies between runs (as with the
+ * reference's atomics).
  *
  * Reference interface replaced: the pybind entries `spmv_forward(row_ptr,
  * col_idx, vals, X) -> Y` and `spmv_backward(row_ptr, col_idx, vals, X,
@@ -74,16 +77,18 @@ int spmv_forward_gather_f32_i64(const int64_t* row_ptr, const int64_t* col_idx,
  * with more than 16384 columns or more than 2^31 - 1 nonzeros; dX is then
  * accumulated with fp32 atomics).  The workspace is scratch: no initial
  * contents, nothing kept; 256-byte aligned.  The size serves int32 and
- * int64 indices alike.  At D > 1 the build of the column-major copy passes
- * column totals between workgroups through nonce-tagged slots (one launch,
- * no clearing); while `stream` is being captured into a HIP graph a small
- * fill kernel clears those slots first. */
+ * int64 indices alike.  At D > 1 the size covers both dX routes (which one
+ * a call takes depends on the alignment of its arrays); the build of the
+ * column-major copy passes column totals between workgroups through
+ * nonce-tagged slots (one launch, no clearing); while `stream` is being
+ * captured into a HIP graph a small fill kernel clears those slots first. */
 size_t spmv_backward_workspace_bytes(int64_t M, int64_t K, int64_t D, int64_t nnz);
 
 /* Byte offset in that workspace of a uint32 trip counter for shapes that
  * take the D > 1 column-major route (SIZE_MAX otherwise): a workgroup's wait
  * for the column totals of the workgroups before it has a spin cap, never
- * expected to fire; a trip adds 1 here and leaves dX wrong.  The library
+ * expected to fire; a trip adds 1 here and leaves dX wrong (the
+ * column-block route has no such wait and leaves the counter alone).  The library
  * never clears it: a caller that wants to detect a trip zeroes it before
  * the call and reads it after. */
 size_t spmv_status_offset(int64_t M, int64_t K, int64_t D, int64_t nnz);
@@ -92,7 +97,8 @@ size_t spmv_status_offset(int64_t M, int64_t K, int64_t D, int64_t nnz);
  * `spmv_backward`).  Either output may be NULL to skip it; dX is fully
  * written.  When dX is requested, the workspace must hold
  * spmv_backward_workspace_bytes() bytes: at D == 1 dX = A^T dY is summed by
- * column bucket there, at D > 1 it holds the column-major copy of A. */
+ * column bucket there, at D > 1 it holds the entries ordered by column
+ * (per chunk by column block, or the column-major copy of A). */
 int spmv_backward_f32_i32(const int32_t* row_ptr, const int32_t* col_idx, const float* vals,
                           const float* X, const float* dY, float* dvals, float* dX,
                           int64_t M, int64_t K, int64_t D, int64_t nnz, void* workspace,

@@ -43,13 +43,17 @@
 //    64), float4 columns when D % 4 == 0 and X / Y are 16-byte aligned; the
 //    lanes of a group share each (col, val) load and read the X row
 //    coalesced, and G groups split a long row's nonzeros (their sums added
-//    by an xor butterfly).  Backward (K <= 16384): dX = A^T dY through a
-//    stable column-major copy of A built in the workspace (chunk histograms,
-//    column offsets, an in-order scatter), then the same lane-group gather
-//    per column, with dvals from the same pass; deterministic, no atomics
-//    (the spmm_t_* kernels below).  Beyond 16384
-//    columns: per nonzero a group reduction for dvals and per-element
-//    atomics for dX.
+//    by an xor butterfly).  Backward, deterministic and without atomics:
+//    with D % 4 == 0, D <= 64, at most 256 blocks of 256 / L columns
+//    (K <= 4096 at the reference default) and 16-byte aligned X / dY / dX,
+//    two launches: each 1024-position chunk sorts its entries by column
+//    block in LDS, then each column block gathers its segment of every chunk
+//    and sums dY rows per column in registers (the spmm_b_* kernels); else,
+//    up to K = 16384, a stable column-major copy of A built in the workspace
+//    (chunk histograms, column offsets, an in-order scatter), then the same
+//    lane-group gather per column (the spmm_t_* kernels); dvals from the
+//    gather pass either way.  Beyond 16384 columns: per nonzero a group
+//    reduction for dvals and per-element atomics for dX.
 #include <algorithm>
 #include <cstdint>
 #include <type_traits>
@@ -1281,6 +1285,410 @@ __global__ __launch_bounds__(kThreads) void spmm_t_gather_kernel(
   }
 }
 
+// ---------------------- SpMM backward dX by column blocks (D > 1, K small)
+// dX = A^T dY in two launches, without a global column histogram, for at most
+// kBktMaxKeys blocks of Kb = 256 / L columns (K <= 4096 at 16 < D <= 64,
+// K <= 16384 at D <= 16; D % 4 == 0, one float4 per lane; the reference's
+// default SpMM is M = K = 4096, D = 64).
+//  C1 spmm_b_sort_kernel:   chunk w = positions [w kBktChunk, (w+1) kBktChunk),
+//                           one workgroup each: every position's row (as in
+//                           S3), then a stable LDS sort of the chunk's
+//                           entries by column block (two 4-bit radix passes,
+//                           ballot ranks), written back in place as 16-byte
+//                           records {row, position, value, column}, with
+//                           off[w][k] = the first record of block k.
+//  C2 spmm_b_gather_kernel: column block b, one workgroup each: block b's
+//                           segment of every chunk (in chunk order, so in
+//                           position order) copied to LDS, ordered by column
+//                           (a stable counting sort with ballot ranks), and
+//                           lane group j (L lanes) sums vals * dY[row] over
+//                           column b Kb + j's entries, 16 per step, in
+//                           registers (and forms dvals[p] = dY[row] . X[c]);
+//                           up to kBktCap entries per round.
+// Each dX row is summed in position order, so dX is bitwise repeatable.
+constexpr int kBktChunk = 1024;
+constexpr int kBktThreads = 512;
+constexpr int kBktWaves = kBktThreads / 64;
+constexpr int kBktMaxKeys = 256;
+constexpr int kBktCap = 2048;
+constexpr int kBktE = 16;  // entries per lane-group step
+
+__device__ __forceinline__ int ranks_below(unsigned long long b) {
+  return __builtin_amdgcn_mbcnt_hi((unsigned)(b >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)b, 0));
+}
+
+// Stable counting sort of n <= kBktWaves * 64 * R entries by digit(e) in
+// [0, S) (S <= 64): wave v takes entries [v n_v, (v+1) n_v) in rounds of 64,
+// counts them per digit (16 or 64 ballots a round), and places them after the
+// entries of lower digits and of earlier waves with the same digit.
+// place(e, slot) moves entry e; cnt: kBktWaves * S ints of LDS; start/len
+// (optional, S ints each) receive each digit's first slot and count.
+template <int S, typename Digit, typename Place>
+__device__ __forceinline__ void ballot_sort(int n, Digit digit, Place place, int* cnt, int* start,
+                                            int* len) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int per = (n + kBktWaves - 1) / kBktWaves;
+  const int e0 = min(n, wave * per), e1 = min(n, e0 + per);
+  int kc = 0;  // lane d: this wave's count of digit d
+  for (int i0 = e0; i0 < e1; i0 += 64) {
+    const int e = i0 + lane;
+    const int dg = e < e1 ? digit(e) : -1;
+#pragma unroll
+    for (int d = 0; d < S; ++d) {
+      const unsigned long long b = __ballot(dg == d);
+      if (lane == d) kc += __popcll(b);
+    }
+  }
+  if (lane < S) cnt[wave * S + lane] = kc;
+  __syncthreads();
+  int tot = 0, before = 0;
+  if (lane < S) {
+#pragma unroll
+    for (int v = 0; v < kBktWaves; ++v) {
+      const int x = cnt[v * S + lane];
+      tot += x;
+      if (v < wave) before += x;
+    }
+  }
+  int incl = tot;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += y;
+  }
+  if (start != nullptr && wave == 0 && lane < S) {
+    start[lane] = incl - tot;
+    len[lane] = tot;
+  }
+  int base = incl - tot + before;  // lane d: the next slot of digit d
+  for (int i0 = e0; i0 < e1; i0 += 64) {
+    const int e = i0 + lane;
+    const bool v = e < e1;
+    const int dg = v ? digit(e) : -1;
+    int rank = 0, inc = 0;
+#pragma unroll
+    for (int d = 0; d < S; ++d) {
+      const unsigned long long b = __ballot(dg == d);
+      if (dg == d) rank = ranks_below(b);
+      if (lane == d) inc = __popcll(b);
+    }
+    const int slot = __shfl(base, dg & 63, 64) + rank;
+    base += inc;
+    if (v) place(e, slot);
+  }
+  __syncthreads();
+}
+
+// Stable ranks of NT * IPT items by a 4-bit digit: thread t holds items
+// t IPT .. t IPT + IPT - 1 (dg[i] < 0 marks an empty slot) and counts them in
+// its own column of cnt[16][NT] (uint16, LDS); an exclusive scan of the
+// counters in digit-major order (16 consecutive counters per thread, then
+// across threads) turns them into starts, and rank = start + the item's
+// count before it.  start16 (optional, 17 ints) receives each digit's first
+// rank and the total.
+template <int NT, int IPT>
+__device__ __forceinline__ void rank16(const int (&dg)[IPT], int (&rank)[IPT],
+                                       unsigned short* cnt, int* wtot, int* start16) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+#pragma unroll
+  for (int d = 0; d < 16; ++d) cnt[d * NT + t] = 0;
+  int local[IPT];
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    local[i] = 0;
+    if (dg[i] >= 0) {
+      unsigned short* c = cnt + dg[i] * NT + t;
+      local[i] = *c;
+      *c = (unsigned short)(local[i] + 1);
+    }
+  }
+  __syncthreads();
+  int run = 0, ex[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    ex[j] = run;
+    run += cnt[t * 16 + j];
+  }
+  int incl = run;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) wtot[wave] = incl;
+  __syncthreads();
+  int base = incl - run;
+#pragma unroll
+  for (int v = 0; v < NT / 64; ++v) base += v < wave ? wtot[v] : 0;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) cnt[t * 16 + j] = (unsigned short)(base + ex[j]);
+  if (start16 != nullptr && (t * 16) % NT == 0) start16[t * 16 / NT] = base;
+  if (start16 != nullptr && t == NT - 1) start16[16] = base + run;
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) rank[i] = dg[i] >= 0 ? cnt[dg[i] * NT + t] + local[i] : -1;
+  __syncthreads();  // cnt is reused by the next call
+}
+
+template <typename I>
+__global__ __launch_bounds__(kBktThreads) void spmm_b_sort_kernel(
+    const I* __restrict__ ptr, const I* __restrict__ col, const float* __restrict__ vals,
+    i32x4_t* __restrict__ crec, int* __restrict__ off, int64_t M, int64_t K, int64_t nnz,
+    int n_keys, int kb_shift) {
+  __shared__ i32x4_t ent[2][kBktChunk];
+  __shared__ int s_win[kScatterRowWin];  // row_ptr[ra + 1 .. rb]
+  __shared__ long long s_rows[2];
+  __shared__ int cnt[kBktWaves * 16];
+  __shared__ unsigned short rcnt[16 * kBktThreads];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t w = blockIdx.x;
+  const int64_t p0 = w * kBktChunk, p1 = min(nnz, p0 + kBktChunk);
+  const int n = (int)(p1 - p0);
+  constexpr int kPerT = kBktChunk / kBktThreads;
+  // waves 0 and 1 find the rows holding positions p0 and p1 - 1 before
+  // issuing their column loads (a wave's loads complete in order, so a
+  // probe issued after them would wait for them); the loads use clamped
+  // addresses, no branches
+  if (wave < 2) {
+    const int64_t r = rows_lower_bound(ptr, M, nnz, wave == 0 ? p0 + 1 : p1, lane, 0) - 1;
+    if (lane == 0) s_rows[wave] = max((int64_t)0, min(r, M - 1));
+  }
+  I craw[kPerT];
+  float vv[kPerT];
+#pragma unroll
+  for (int k = 0; k < kPerT; ++k) {
+    const int64_t q = min(p0 + (int64_t)k * kBktThreads + threadIdx.x, p1 - 1);
+    craw[k] = col[q];
+    vv[k] = vals[q];
+  }
+  __syncthreads();
+  const int64_t ra = s_rows[0], rb = max(s_rows[0], s_rows[1]);
+  const int nw = (int)min(rb - ra, (int64_t)kScatterRowWin + 1);
+  const bool windowed = rb - ra <= kScatterRowWin;
+  if (windowed && rb > ra && threadIdx.x < kThreads) load_to_lds(ptr + ra + 1, s_win, rb - ra);
+  __syncthreads();
+  int top = 1;
+  while (top * 2 <= nw) top *= 2;
+#pragma unroll
+  for (int k = 0; k < kPerT; ++k) {
+    const int e = k * kBktThreads + threadIdx.x;
+    const int64_t q = p0 + e;
+    const int64_t qr = min(q, p1 - 1);
+    int64_t row;
+    if (windowed) {  // row ra + m with s_win[m - 1] = row_ptr[ra + m] <= qr
+      int m = 0;
+      for (int step = top; step > 0; step >>= 1)
+        if (m + step <= nw && s_win[m + step - 1] <= qr) m += step;
+      row = ra + m;
+    } else {
+      row = row_of(ptr, ra, rb, qr, nnz);
+    }
+    const int64_t c = (int64_t)craw[k];
+    const int cl = (int)(c < 0 ? 0 : (c >= K ? K - 1 : c));
+    if (e < n) ent[0][e] = i32x4_t{(int)row, (int)q, __float_as_int(vv[k]), cl};
+  }
+  __syncthreads();
+  // two stable radix passes over the block index c >> kb_shift (< 256);
+  // thread t moves entries 2t and 2t + 1
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    const i32x4_t* src = ent[pass];
+    i32x4_t* dst = ent[pass ^ 1];
+    int dg[2], rk[2];
+    i32x4_t it[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int e = 2 * threadIdx.x + i;
+      it[i] = src[min(e, kBktChunk - 1)];
+      dg[i] = e < n ? (it[i][3] >> (kb_shift + 4 * pass)) & 15 : -1;
+    }
+    rank16<kBktThreads, 2>(dg, rk, rcnt, cnt, nullptr);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      if (rk[i] >= 0) dst[rk[i]] = it[i];
+    __syncthreads();
+  }
+  for (int e = threadIdx.x; e < n; e += kBktThreads) crec[p0 + e] = ent[0][e];
+  // off[w][k]: the first sorted entry whose block is >= k
+  int* ow = off + w * (int64_t)(n_keys + 1);
+  for (int k = threadIdx.x; k <= n_keys; k += kBktThreads) {
+    int lo = 0, hi = n;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if ((ent[0][mid][3] >> kb_shift) < k) lo = mid + 1;
+      else hi = mid;
+    }
+    ow[k] = lo;
+  }
+}
+
+template <int L, bool DV>
+__global__ __launch_bounds__(kBktThreads) void spmm_b_gather_kernel(
+    const i32x4_t* __restrict__ crec, const int* __restrict__ off, const float* __restrict__ X,
+    const float* __restrict__ dY, float* __restrict__ dX, float* __restrict__ dvals, int64_t M,
+    int64_t K, int64_t D, int64_t nnz, int64_t n_chunks, int n_keys) {
+  constexpr int S = kThreads / L;  // columns per block
+  // two lane groups per column: half h of the workgroup takes the column's
+  // steps h, h + 2, ... (kBktE entries each), and the halves' sums are
+  // added in that order at the end
+  __shared__ i32x4_t list[kBktCap];
+  __shared__ unsigned short order[kBktCap];
+  __shared__ int cnt[kBktWaves * 64];
+  __shared__ int gstart[S + 1], glen[S];
+  __shared__ int s_wsum[kBktWaves];
+  __shared__ f32x4 s_half[kThreads];  // the second half's sums
+  __shared__ unsigned short rcnt[S == 16 ? 16 * kBktThreads : 1];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int half = threadIdx.x / kThreads, tl = threadIdx.x % kThreads;
+  const int g = tl / L, gl = tl % L;
+  const int b = blockIdx.x;
+  const int64_t c = (int64_t)b * S + g;
+  const bool live = c < K;
+  const int64_t cc = live ? c : K - 1;
+  const int d = gl * 4;
+  const bool active = d < D;
+  const int64_t dc = active ? d : 0;
+  f32x4 xc = nl2k::zero4();
+  if constexpr (DV) xc = nl2k::load4(X + cc * D + dc);
+  f32x4 acc = nl2k::zero4();
+  const int64_t ostride = n_keys + 1;
+  for (int64_t wa = 0; wa < n_chunks;) {
+    // chunk wa + t's segment of this block, t = thread
+    const int64_t wt = wa + threadIdx.x;
+    int s = 0, len = 0;
+    if (wt < n_chunks) {
+      s = off[wt * ostride + b];
+      len = max(off[wt * ostride + b + 1] - s, 0);
+    }
+    // inclusive scan of the lengths over the workgroup
+    int incl = len;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += y;
+    }
+    if (lane == 63) s_wsum[wave] = incl;
+    __syncthreads();
+#pragma unroll
+    for (int v = 0; v < kBktWaves; ++v) incl += v < wave ? s_wsum[v] : 0;
+    // this round: the leading chunks whose entries fit kBktCap (the first
+    // always does: a chunk has at most kBktChunk <= kBktCap entries)
+    const bool take = incl <= kBktCap && wt < n_chunks;
+    const int n_take = __syncthreads_count(take);
+    const int excl = incl - len;
+    if (take) {  // four loads in flight at a time
+      const i32x4_t* src = crec + wt * kBktChunk + s;
+      for (int i = 0; i < len; i += 4) {
+        i32x4_t v4[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v4[u] = src[min(i + u, len - 1)];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (i + u < len) list[excl + i + u] = v4[u];
+      }
+    }
+    if (take && threadIdx.x == n_take - 1) s_wsum[0] = incl;  // the round's entry count
+    __syncthreads();
+    const int T = s_wsum[0];
+    if constexpr (S == 16) {
+      // entries by column: thread t ranks entries t IPT .. t IPT + IPT - 1
+      constexpr int IPT = kBktCap / kBktThreads;
+      int dg[IPT], rk[IPT];
+#pragma unroll
+      for (int i = 0; i < IPT; ++i) {
+        const int e = threadIdx.x * IPT + i;
+        dg[i] = e < T ? (list[e][3] & 15) : -1;
+      }
+      rank16<kBktThreads, IPT>(dg, rk, rcnt, cnt, gstart);
+#pragma unroll
+      for (int i = 0; i < IPT; ++i)
+        if (rk[i] >= 0) order[rk[i]] = (unsigned short)(threadIdx.x * IPT + i);
+      __syncthreads();
+    } else {
+      ballot_sort<S>(
+          T, [&](int e) { return list[e][3] & (S - 1); },
+          [&](int e, int slot) { order[slot] = (unsigned short)e; }, cnt, gstart, glen);
+    }
+    // column c's entries of the round: this half's steps
+    const int q0 = gstart[g], qn = S == 16 ? gstart[g + 1] - q0 : glen[g];
+    for (int q = half * kBktE; q < qn; q += 2 * kBktE) {
+      i32x4_t r[kBktE];
+#pragma unroll
+      for (int u = 0; u < kBktE; ++u) r[u] = list[order[q0 + min(q + u, qn - 1)]];
+      f32x4 gy[kBktE];
+#pragma unroll
+      for (int u = 0; u < kBktE; ++u) {
+        const int64_t row = min(max((int64_t)r[u][0], (int64_t)0), M - 1);
+        gy[u] = nl2k::load4(dY + row * D + dc);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < kBktE; ++u)
+        if (q + u < qn) acc += __int_as_float(r[u][2]) * gy[u];
+      if constexpr (DV) {
+        // reduce-scatter of the kBktE dots over the group's L lanes: lane gl
+        // ends with the dots of entries gl * kBktE / L .. + kBktE / L - 1
+        float v[kBktE];
+#pragma unroll
+        for (int u = 0; u < kBktE; ++u) {
+          const f32x4 y = gy[u];
+          v[u] = active ? (y[0] * xc[0] + y[1] * xc[1]) + (y[2] * xc[2] + y[3] * xc[3]) : 0.f;
+        }
+        // Each level pairs every lane with a partner whose lane bit m
+        // differs, through a DPP move inside the 16-lane row: row_mirror
+        // (l <-> 15 - l) for m = 8, row_half_mirror (l <-> 7 - l within each
+        // half row) for m = 4, quad_perm xor 2 and xor 1; the lane with bit
+        // m set keeps the upper half of its entries.  A group is a DPP row
+        // (L = 16) or a quad (L = 4), so partners never leave it, and the
+        // pairs of the successive levels span the group.
+        auto level = [&](auto ctlc, auto mc, auto hc) {
+          constexpr int ctl = decltype(ctlc)::value, m = decltype(mc)::value,
+                        h = decltype(hc)::value;
+          const bool upper = (gl & m) != 0;
+#pragma unroll
+          for (int k = 0; k < h; ++k) {
+            const float keep = upper ? v[k + h] : v[k];
+            const float send = upper ? v[k] : v[k + h];
+            v[k] = keep + nl2k::dpp_mov<ctl>(send);
+          }
+        };
+        using C_MIR = std::integral_constant<int, 0x140>;
+        using C_HMIR = std::integral_constant<int, 0x141>;
+        using C_X2 = std::integral_constant<int, 0x4E>;
+        using C_X1 = std::integral_constant<int, 0xB1>;
+        using IC8 = std::integral_constant<int, 8>;
+        using IC4 = std::integral_constant<int, 4>;
+        using IC2 = std::integral_constant<int, 2>;
+        using IC1 = std::integral_constant<int, 1>;
+        static_assert(kBktE == 16, "levels below are written out for 16 entries");
+        if constexpr (L == 16) {
+          level(C_MIR{}, IC8{}, IC8{});
+          level(C_HMIR{}, IC4{}, IC4{});
+          level(C_X2{}, IC2{}, IC2{});
+          level(C_X1{}, IC1{}, IC1{});
+        } else {
+          level(C_X2{}, IC2{}, IC8{});
+          level(C_X1{}, IC1{}, IC4{});
+        }
+        constexpr int per = kBktE / L;
+#pragma unroll
+        for (int j = 0; j < per; ++j) {
+          const int u = gl * per + j;
+          if (q + u < qn) {
+            const int64_t p = min(max((int64_t)list[order[q0 + q + u]][1], (int64_t)0), nnz - 1);
+            dvals[p] = v[j];
+          }
+        }
+      }
+    }
+    wa += n_take;
+    __syncthreads();  // the list is rewritten by the next round
+  }
+  if (half == 1) s_half[tl] = acc;
+  __syncthreads();
+  if (half == 0 && live && active) nl2k::store4(dX + c * D + d, acc + s_half[tl]);
+}
+
 // ------------------------------ D == 1 dX: contributions formed in the sort
 // tile_rows[t] for t in [0, n_tiles]: the last row r with row_ptr[r] <=
 // min(t * kSortTile, nnz - 1), clamped into [0, M - 1] -- the row holding
@@ -1827,11 +2235,68 @@ TransposePlan transpose_plan(int64_t M, int64_t K, int64_t D, int64_t nnz, size_
   return p;
 }
 
+// dX by column blocks (spmm_b_* kernels): D > 1, D % 4 == 0, D <= 64, at
+// most kBktMaxKeys blocks of 256 / L columns, nnz < 2^31.  Workspace: the
+// first 256 bytes are left alone (the transposed route's trip counter lives
+// there, so its offset is the same whichever route a call takes), then the
+// records [nnz] (16 B) and off [n_chunks][n_keys + 1] (int32).
+struct ColBlockPlan {
+  bool use = false;
+  int L = 0, n_keys = 0, kb_shift = 0;
+  int64_t n_chunks = 0;
+  size_t off_rec = 256, off_off = 0, bytes = 0;
+};
+
+ColBlockPlan col_block_plan(int64_t M, int64_t K, int64_t D, int64_t nnz) {
+  ColBlockPlan p;
+  if (D <= 1 || D > 64 || D % 4 != 0 || M <= 0 || M > INT32_MAX || nnz <= 0 || nnz > INT32_MAX)
+    return p;
+  const int L = D <= 16 ? 4 : 16;
+  const int kb = kThreads / L;
+  const int64_t n_keys = nl2k::ceil_div(K, (int64_t)kb);
+  if (n_keys > kBktMaxKeys) return p;
+  p.use = true;
+  p.L = L;
+  p.n_keys = (int)n_keys;
+  p.kb_shift = __builtin_ctz(kb);
+  p.n_chunks = nl2k::ceil_div(nnz, (int64_t)kBktChunk);
+  p.off_off = p.off_rec + align256((size_t)nnz * 16);
+  p.bytes = p.off_off + align256((size_t)p.n_chunks * (size_t)(n_keys + 1) * sizeof(int));
+  return p;
+}
+
 template <typename I>
 size_t workspace_bytes_for(int64_t M, int64_t K, int64_t D, int64_t nnz) {
   if (M <= 0) return 0;
   if (D == 1) return bucket_plan(K, D, nnz).bytes;
-  return transpose_plan(M, K, D, nnz, sizeof(I)).bytes;
+  // the column-block route needs 16-byte aligned X, dY and dX, known only at
+  // the call: room for either route
+  const ColBlockPlan cp = col_block_plan(M, K, D, nnz);
+  return std::max(cp.use ? cp.bytes : (size_t)0, transpose_plan(M, K, D, nnz, sizeof(I)).bytes);
+}
+
+template <typename I>
+int col_block_backward(const ColBlockPlan& cp, const I* ptr, const I* col, const float* vals,
+                       const float* X, const float* dY, float* dvals, float* dX, int64_t M,
+                       int64_t K, int64_t D, int64_t nnz, char* ws, hipStream_t stream,
+                       const char* who) {
+  i32x4_t* crec = reinterpret_cast<i32x4_t*>(ws + cp.off_rec);
+  int* off = reinterpret_cast<int*>(ws + cp.off_off);
+  hipLaunchKernelGGL((spmm_b_sort_kernel<I>), dim3((unsigned)cp.n_chunks), dim3(kBktThreads), 0,
+                     stream, ptr, col, vals, crec, off, M, K, nnz, cp.n_keys, cp.kb_shift);
+  int st = nl2k::check_launch(who);
+  if (st) return st;
+  const dim3 grid((unsigned)cp.n_keys), block(kBktThreads);
+#define SPMM_B(LL, DVV)                                                                      \
+  hipLaunchKernelGGL((spmm_b_gather_kernel<LL, DVV>), grid, block, 0, stream, crec, off, X, dY, \
+                     dX, dvals, M, K, D, nnz, cp.n_chunks, cp.n_keys)
+  if (cp.L == 4) {
+    if (dvals) SPMM_B(4, true); else SPMM_B(4, false);
+  } else {
+    if (dvals) SPMM_B(16, true); else SPMM_B(16, false);
+  }
+#undef SPMM_B
+  return nl2k::check_launch(who);
 }
 
 template <typename I>
@@ -1977,6 +2442,16 @@ int backward(const I* ptr, const I* col, const float* vals, const float* X, cons
     hipLaunchKernelGGL(spmv_bucket_sum_kernel, dim3((unsigned)bp.nb), dim3(kSumThreads), 0,
                        stream, contrib, low, meta, bp.n_tiles, bp.nb, bp.cols, K, nnz, dX);
     return nl2k::check_launch(who);
+  }
+  const ColBlockPlan cp = col_block_plan(M, K, D, nnz);
+  if (dX && cp.use && nl2k::aligned16(X) && nl2k::aligned16(dY) && nl2k::aligned16(dX)) {
+    if (!workspace || ws_bytes < cp.bytes)
+      return nl2k::fail(NL2K_ERR_WORKSPACE, "%s: workspace of %zu bytes required, got %zu", who,
+                        cp.bytes, workspace ? ws_bytes : (size_t)0);
+    if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+      return nl2k::fail(NL2K_ERR_ALIGN, "%s: workspace must be 256-byte aligned", who);
+    return col_block_backward<I>(cp, ptr, col, vals, X, dY, dvals, dX, M, K, D, nnz,
+                                 static_cast<char*>(workspace), stream, who);
   }
   const TransposePlan tp = transpose_plan(M, K, D, nnz, sizeof(I));
   if (dX && tp.use) {

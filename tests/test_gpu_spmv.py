@@ -325,6 +325,74 @@ def test_spmv_misaligned_values():
     _close("y (misaligned X)", y, osp.forward_f64(ptr.numpy(), col.numpy(), vals.numpy(), X.numpy()))
 
 
+def _backward_twice(ptr, col, vals, X, dY, X_dev=None, dY_dev=None):
+    """Two backward calls; asserts they agree bit for bit and returns one."""
+    from cases.spmv import op
+    args = [ptr.cuda(), col.cuda(), vals.cuda(), X.cuda() if X_dev is None else X_dev]
+    g = dY.cuda() if dY_dev is None else dY_dev
+    dv1, dX1 = op.spmv_backward(*args, g)
+    dv2, dX2 = op.spmv_backward(*args, g)
+    torch.cuda.synchronize()
+    assert torch.equal(dX1, dX2), "dX is not bitwise repeatable"
+    assert torch.equal(dv1, dv2), "dvals is not bitwise repeatable"
+    return dv1, dX1
+
+
+@pytest.mark.parametrize("k,d", [(20, 64), (20, 8), (40, 16)])
+def test_spmm_column_block_rounds(k, d):
+    """Few columns, many nonzeros: one column block holds tens of thousands
+    of entries, which the column-block gather takes in several rounds of at
+    most 2048 (K = 20 at D = 8: one block of 64 columns holds every entry).
+    dX matches the oracle and repeats bit for bit."""
+    announce(f"spmm column-block rounds K={k} D={d}")
+    for idx in (torch.int64, torch.int32):
+        ptr, col, vals, X = _csr(np.full(4000, 10), k, d, 77, idx)
+        dY = torch.randn(4000, d, generator=torch.Generator().manual_seed(78))
+        dv, dX = _backward_twice(ptr, col, vals, X, dY)
+        rdv, rdX = osp.backward_f64(ptr.numpy(), col.numpy(), vals.numpy(), X.numpy(), dY.numpy())
+        _close("dvals", dv, rdv)
+        _close("dX", dX, rdX)
+
+
+@pytest.mark.parametrize("d", [64, 16])
+def test_spmm_column_block_many_chunks(d):
+    """More 1024-position sort chunks (563) than one gather round reads
+    (512 per window): the window moves on, and rows with zero to 128
+    entries cross chunk edges."""
+    announce(f"spmm column-block chunk windows D={d}")
+    lens = np.random.default_rng(90).integers(0, 129, 9000)
+    ptr, col, vals, X = _csr(lens, 4096, d, 91, torch.int32)
+    assert vals.numel() > 512 * 1024
+    dY = torch.randn(9000, d, generator=torch.Generator().manual_seed(92))
+    dv, dX = _backward_twice(ptr, col, vals, X, dY)
+    rdv, rdX = osp.backward_f64(ptr.numpy(), col.numpy(), vals.numpy(), X.numpy(), dY.numpy())
+    _close("dvals", dv, rdv)
+    _close("dX", dX, rdX)
+
+
+def test_spmm_backward_routes_agree():
+    """The reference default shape through both D > 1 routes: 16-byte
+    aligned X and dY take the column-block kernels, an X that starts one
+    float past an aligned address takes the column-major copy.  Each is
+    bitwise repeatable and matches the oracle, and they agree with each
+    other to rounding."""
+    announce("spmm backward: column-block route vs column-major copy")
+    from cases.spmv import reference as ref
+    t = ref.make_inputs(3, torch.float32, "cpu")
+    ptr, col, vals, X = (t[k] for k in ("row_ptr", "col_idx", "vals", "X"))
+    K, D = X.shape
+    dY = torch.randn(ptr.numel() - 1, D, generator=torch.Generator().manual_seed(93))
+    dv_a, dX_a = _backward_twice(ptr, col, vals, X, dY)
+    xb = torch.empty(X.numel() + 1, device="cuda")
+    xb[1:].copy_(X.reshape(-1).cuda())
+    dv_b, dX_b = _backward_twice(ptr, col, vals, X, dY, X_dev=xb[1:].view(K, D))
+    rdv, rdX = osp.backward_f64(ptr.numpy(), col.numpy(), vals.numpy(), X.numpy(), dY.numpy())
+    for name, dv, dX in (("blocks", dv_a, dX_a), ("column-major", dv_b, dX_b)):
+        _close(f"dvals ({name})", dv, rdv)
+        _close(f"dX ({name})", dX, rdX)
+    assert torch.allclose(dX_a, dX_b, atol=1e-4, rtol=1e-4)
+
+
 @pytest.mark.parametrize("opt_in", ["default", "params", "env"])
 def test_spmv_autograd_saved_tensors_and_gathered_opt_in(opt_in, monkeypatch):
     """The reference's save list (cases/spmv/op.py:28-33) by default: exactly
