@@ -101,13 +101,16 @@ __global__ __launch_bounds__(kBlock) void peak_mfma_f32_kernel(float* __restrict
 constexpr int kCoN = 4096;
 constexpr int kCoLds = 96 * 1024;
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-__global__ __launch_bounds__(768) void peak_coexec_kernel(
+template <int NS>
+__global__ __launch_bounds__(1024) void peak_coexec_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ out,
-    unsigned long long* __restrict__ ticks, int tiles, int kind, int mfma_iters, int direct) {
+    unsigned long long* __restrict__ ticks, int tiles, int kind, int mfma_iters, int direct,
+    int mfma_waves) {
   extern __shared__ float co_lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ri = blockIdx.x / 16, rj = blockIdx.x % 16;
+  if (wave < 8 && wave >= mfma_waves) return;  // idle MFMA slot
   if (wave < 8) {
     const unsigned long long m0 = __builtin_amdgcn_s_memrealtime();
     const float a = 1e-3f * (float)lane, b = 1.0f;
@@ -138,39 +141,164 @@ __global__ __launch_bounds__(768) void peak_coexec_kernel(
       for (int j = 0; j < 4; ++j) s += acc[j][0];
     }
     const unsigned long long m1 = __builtin_amdgcn_s_memrealtime();
-    if (lane == 0 && blockIdx.x < 256) ticks[1024 + 8 * blockIdx.x + wave] = m1 - m0;
+    if (lane == 0 && blockIdx.x < 256) ticks[2048 + 8 * blockIdx.x + wave] = m1 - m0;
     if (s == 1234.5f) out[0] = s;
     return;
   }
+  // NS staging waves share each 64 x 64 tile pair: 64 / NS rows each, as
+  // NL = 16 / NS loads of four rows per array
+  constexpr int NL = 16 / NS;
   const int w = wave - 8;
   const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
   for (int it = 0; it < tiles; ++it) {
     const int t = it % 16, ic = t / 4, jc = t % 4;
-    const int row0 = ri * 256 + ic * 64 + w * 16 + (lane >> 4);
+    const int row0 = ri * 256 + ic * 64 + w * (64 / NS) + (lane >> 4);
     const int col = rj * 256 + jc * 64 + (lane & 15) * 4;
-    float* st = co_lds + (it & 1) * 8192 + w * 2048;
+    float* st = co_lds + (it & 1) * 8192 + w * (8192 / NS);
     if (direct) {
+#pragma unroll
+      for (int s = 0; s < NL; ++s) {
+        __builtin_amdgcn_global_load_lds(A + (size_t)(row0 + 4 * s) * kCoN + col, st + s * 256, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(B + (size_t)(row0 + 4 * s) * kCoN + col, st + (NL + s) * 256, 16, 0, 0);
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else {
+      f32x4 v[2 * NL];
+#pragma unroll
+      for (int s = 0; s < NL; ++s) {
+        v[s] = *reinterpret_cast<const f32x4*>(A + (size_t)(row0 + 4 * s) * kCoN + col);
+        v[NL + s] = *reinterpret_cast<const f32x4*>(B + (size_t)(row0 + 4 * s) * kCoN + col);
+      }
+#pragma unroll
+      for (int s = 0; s < 2 * NL; ++s) *reinterpret_cast<f32x4*>(st + s * 256 + lane * 4) = v[s];
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+  }
+  const unsigned long long t1 = __builtin_amdgcn_s_memrealtime();
+  if (lane == 0 && blockIdx.x < 256) ticks[NS * blockIdx.x + w] = t1 - t0;
+  if (co_lds[lane] == 1234.5f) out[1] = co_lds[lane + 64];
+}
+
+// Joint-time variant of the co-execution probe: per SIMD, `simd_iters`
+// rounds of 8 fp32 16x16x4 MFMA chains split evenly over mfma_waves / 4
+// waves (1 or 2 per SIMD), beside one staging wave that streams `tiles`
+// 64 x 64 tile pairs straight into LDS with `depth` tile pairs in flight
+// (its waits leave the younger tiles' loads outstanding).  ticks[4 b + w]
+// gets workgroup b's span from its first wave's start to its last wave's
+// end (w = 0), the staging wave's time (w = 1) and the slowest MFMA wave's
+// time (w = 2), in 100 MHz ticks.
+template <int DEPTH>
+__global__ __launch_bounds__(768) void peak_joint_kernel(
+    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ out,
+    unsigned long long* __restrict__ ticks, int tiles, int simd_iters, int mfma_waves,
+    int inline_stage) {
+  extern __shared__ float co_lds[];
+  __shared__ unsigned long long s_t[12][2];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ri = blockIdx.x / 16, rj = blockIdx.x % 16;
+  const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+  if (inline_stage) {
+    // waves 0-3 run all of their SIMD's MFMA rounds and stage their quarter
+    // of every tile pair themselves, one tile's loads per simd_iters / tiles
+    // rounds, with DEPTH tile pairs in flight
+    if (wave < 4) {
+      const int w = wave;
+      const int per = simd_iters / tiles;
+      const float a = 1e-3f * (float)lane, b = 1.0f;
+      f32x4 acc[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = nl2k::zero4();
+      auto issue = [&](int it) {
+        const int t = it % 16, ic = t / 4, jc = t % 4;
+        const int row0 = ri * 256 + ic * 64 + w * 16 + (lane >> 4);
+        const int col = rj * 256 + jc * 64 + (lane & 15) * 4;
+        float* st = co_lds + (it % DEPTH) * 8192 + w * 2048;
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) {
+          __builtin_amdgcn_global_load_lds(A + (size_t)(row0 + 4 * s2) * kCoN + col, st + s2 * 256, 16, 0, 0);
+          __builtin_amdgcn_global_load_lds(B + (size_t)(row0 + 4 * s2) * kCoN + col, st + (4 + s2) * 256, 16, 0, 0);
+        }
+      };
+      for (int it = 0; it < DEPTH - 1 && it < tiles; ++it) issue(it);
+      for (int it = 0; it < tiles; ++it) {
+        if (it + DEPTH - 1 < tiles) issue(it + DEPTH - 1);
+        for (int i = 0; i < per; ++i) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[j] = nl2k::mfma16x4(a, b, acc[j]);
+        }
+        if (it + DEPTH - 1 < tiles) {
+          if constexpr (DEPTH == 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+          else asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        } else {
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+      }
+      float sum = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sum += acc[j][0];
+      if (sum == 1234.5f || co_lds[lane] == 1234.5f) out[0] = sum;
+    }
+  } else if (wave < 8) {
+    if (wave < mfma_waves) {
+      const int iters = simd_iters / (mfma_waves / 4);
+      const float a = 1e-3f * (float)lane, b = 1.0f;
+      f32x4 acc[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = nl2k::zero4();
+      for (int i = 0; i < iters; ++i) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = nl2k::mfma16x4(a, b, acc[j]);
+      }
+      float sum = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sum += acc[j][0];
+      if (sum == 1234.5f) out[0] = sum;
+    }
+  } else if (wave < 12) {
+    const int w = wave - 8;
+    auto issue = [&](int it) {
+      const int t = it % 16, ic = t / 4, jc = t % 4;
+      const int row0 = ri * 256 + ic * 64 + w * 16 + (lane >> 4);
+      const int col = rj * 256 + jc * 64 + (lane & 15) * 4;
+      float* st = co_lds + (it % DEPTH) * 8192 + w * 2048;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         __builtin_amdgcn_global_load_lds(A + (size_t)(row0 + 4 * s) * kCoN + col, st + s * 256, 16, 0, 0);
         __builtin_amdgcn_global_load_lds(B + (size_t)(row0 + 4 * s) * kCoN + col, st + (4 + s) * 256, 16, 0, 0);
       }
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    } else {
-      f32x4 v[8];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        v[s] = *reinterpret_cast<const f32x4*>(A + (size_t)(row0 + 4 * s) * kCoN + col);
-        v[4 + s] = *reinterpret_cast<const f32x4*>(B + (size_t)(row0 + 4 * s) * kCoN + col);
+    };
+    for (int it = 0; it < DEPTH - 1 && it < tiles; ++it) issue(it);
+    for (int it = 0; it < tiles; ++it) {
+      if (it + DEPTH - 1 < tiles) {
+        issue(it + DEPTH - 1);
+        // tile it's 8 loads are the oldest: DEPTH - 1 younger tiles stay out
+        if constexpr (DEPTH == 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+      } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       }
-#pragma unroll
-      for (int s = 0; s < 8; ++s) *reinterpret_cast<f32x4*>(st + s * 256 + lane * 4) = v[s];
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
+    if (co_lds[lane] == 1234.5f) out[1] = co_lds[lane + 64];
   }
   const unsigned long long t1 = __builtin_amdgcn_s_memrealtime();
-  if (lane == 0 && blockIdx.x < 256) ticks[4 * blockIdx.x + w] = t1 - t0;
-  if (co_lds[lane] == 1234.5f) out[1] = co_lds[lane + 64];
+  if (lane == 0) {
+    s_t[wave][0] = t0;
+    s_t[wave][1] = t1;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0 && blockIdx.x < 256) {
+    unsigned long long lo = s_t[0][0], hi = s_t[0][1], mf = 0;
+    for (int v = 0; v < 12; ++v) {
+      lo = s_t[v][0] < lo ? s_t[v][0] : lo;
+      hi = s_t[v][1] > hi ? s_t[v][1] : hi;
+      const int mw = inline_stage ? 4 : mfma_waves;
+      if (v < 8 && v < mw && s_t[v][1] - s_t[v][0] > mf) mf = s_t[v][1] - s_t[v][0];
+    }
+    ticks[4 * blockIdx.x] = hi - lo;
+    ticks[4 * blockIdx.x + 1] = inline_stage ? mf : s_t[8][1] - s_t[8][0];
+    ticks[4 * blockIdx.x + 2] = mf;
+  }
 }
 
 bool bad_stream_args(int64_t n4, int blocks) { return n4 < 1 || blocks < 1 || blocks > (1 << 20); }
@@ -226,17 +354,51 @@ int peaks_mfma_f32(float* out, unsigned long long* clk, int blocks, int iters,
 }
 
 // Co-execution probe (peak_coexec_kernel): A and B are [4096, 4096] fp32,
-// out holds 2 floats, ticks 3072 values; blocks <= 256 (one per CU).
+// out holds 2 floats, ticks 4096 values; blocks <= 256 (one per CU).
+// mfma_waves (4 or 8) of the eight MFMA slots run MFMAs (4: one wave per
+// SIMD); stagers (4 or 8) staging waves follow them.
 int peaks_coexec(const float* A, const float* B, float* out, unsigned long long* ticks, int blocks,
-                 int tiles, int kind, int mfma_iters, int direct, hipStream_t stream) {
+                 int tiles, int kind, int mfma_iters, int direct, int mfma_waves, int stagers,
+                 hipStream_t stream) {
   if (!A || !B || !out || !ticks || blocks < 1 || blocks > 256 || tiles < 1 || kind < 0 ||
-      kind > 2 || mfma_iters < 0 || (direct != 0 && direct != 1))
+      kind > 2 || mfma_iters < 0 || (direct != 0 && direct != 1) ||
+      (mfma_waves != 4 && mfma_waves != 8) || (stagers != 4 && stagers != 8))
     return nl2k::fail(NL2K_ERR_SHAPE, "peaks_coexec: bad arguments");
-  int st = nl2k::raise_dynamic_lds((const void*)&peak_coexec_kernel, kCoLds);
+  const void* fn = stagers == 4 ? (const void*)&peak_coexec_kernel<4> : (const void*)&peak_coexec_kernel<8>;
+  int st = nl2k::raise_dynamic_lds(fn, kCoLds);
   if (st) return st;
-  hipLaunchKernelGGL(peak_coexec_kernel, dim3(blocks), dim3(768), kCoLds, stream, A, B, out, ticks,
-                     tiles, kind, mfma_iters, direct);
+  const dim3 block(64 * (8 + stagers));
+  if (stagers == 4)
+    hipLaunchKernelGGL(peak_coexec_kernel<4>, dim3(blocks), block, kCoLds, stream, A, B, out, ticks,
+                       tiles, kind, mfma_iters, direct, mfma_waves);
+  else
+    hipLaunchKernelGGL(peak_coexec_kernel<8>, dim3(blocks), block, kCoLds, stream, A, B, out, ticks,
+                       tiles, kind, mfma_iters, direct, mfma_waves);
   return nl2k::check_launch("peaks_coexec");
+}
+
+// Joint-time probe (peak_joint_kernel): A and B as for peaks_coexec, ticks
+// 1024 values; depth 2 or 3 tile pairs in flight; simd_iters even.
+// inline_stage: the MFMA waves (4, one per SIMD) stage the tiles themselves
+// between their rounds (simd_iters a multiple of tiles) and waves 8-11 idle.
+int peaks_joint(const float* A, const float* B, float* out, unsigned long long* ticks, int blocks,
+                int tiles, int simd_iters, int mfma_waves, int depth, int inline_stage,
+                hipStream_t stream) {
+  if (!A || !B || !out || !ticks || blocks < 1 || blocks > 256 || tiles < 1 || simd_iters < 0 ||
+      (simd_iters & 1) || (mfma_waves != 0 && mfma_waves != 4 && mfma_waves != 8) ||
+      (depth != 2 && depth != 3) || (inline_stage != 0 && inline_stage != 1) ||
+      (inline_stage && (mfma_waves != 4 || simd_iters % tiles != 0)))
+    return nl2k::fail(NL2K_ERR_SHAPE, "peaks_joint: bad arguments");
+  const void* fn = depth == 2 ? (const void*)&peak_joint_kernel<2> : (const void*)&peak_joint_kernel<3>;
+  int st = nl2k::raise_dynamic_lds(fn, kCoLds);
+  if (st) return st;
+  if (depth == 2)
+    hipLaunchKernelGGL(peak_joint_kernel<2>, dim3(blocks), dim3(768), kCoLds, stream, A, B, out,
+                       ticks, tiles, simd_iters, mfma_waves, inline_stage);
+  else
+    hipLaunchKernelGGL(peak_joint_kernel<3>, dim3(blocks), dim3(768), kCoLds, stream, A, B, out,
+                       ticks, tiles, simd_iters, mfma_waves, inline_stage);
+  return nl2k::check_launch("peaks_joint");
 }
 
 }  // extern "C"

@@ -70,7 +70,8 @@ def bind_library(lib):
     capi.bind(lib, "peaks_copy_f32x4", [V, V, I64, I, V])
     capi.bind(lib, "peaks_mfma_f32_flops", [I, I], capi.c_double)
     capi.bind(lib, "peaks_mfma_f32", [V, V, I, I, V])
-    capi.bind(lib, "peaks_coexec", [V, V, V, V, I, I, I, I, I, V])
+    capi.bind(lib, "peaks_coexec", [V, V, V, V, I, I, I, I, I, I, I, V])
+    capi.bind(lib, "peaks_joint", [V, V, V, V, I, I, I, I, I, I, V])
     capi.bind_last_error(lib, "peaks_last_error")
     return lib
 
@@ -162,7 +163,8 @@ def coexec(iters, tiles=64, mfma_iters=3840):
     """Staging waves beside fp32 MFMA waves on every CU (peak_coexec_kernel):
     the stagers' time per 32 KB tile pair and the MFMA waves' rate, for no
     MFMA, 16x16x4 and 32x32x2 MFMAs, staging through registers or straight
-    into LDS.  Prints one JSON line per configuration and a table."""
+    into LDS, with one or two MFMA waves and one or two staging waves per
+    SIMD.  Prints one JSON line per configuration and a table."""
     import torch
     dev = torch.device("cuda:0")
     lib = _lib()
@@ -172,37 +174,91 @@ def coexec(iters, tiles=64, mfma_iters=3840):
     A = torch.ones(n * n, device=dev)
     B = torch.ones(n * n, device=dev)
     out = torch.zeros(2, device=dev)
-    ticks = torch.zeros(3072, dtype=torch.int64, device=dev)
+    ticks = torch.zeros(4096, dtype=torch.int64, device=dev)
     blocks = min(256, torch.cuda.get_device_properties(dev).multi_processor_count)
     flops_per = {1: 2.0 * 16 * 16 * 4, 2: 2.0 * 32 * 32 * 2}
     names = {0: "none", 1: "16x16x4", 2: "32x32x2"}
+    configs = [(kind, direct, 8, 4) for kind in (0, 1, 2) for direct in (0, 1)]
+    configs += [(1, direct, mw, ns) for direct in (0, 1) for mw, ns in ((4, 4), (8, 8), (4, 8))]
     rows = []
-    for kind in (0, 1, 2):
-        for direct in (0, 1):
-            tile_ns, mfma_tf = [], []
-            for _ in range(iters):
-                capi.check(lib.peaks_coexec(P(A), P(B), P(out), P(ticks), blocks, tiles, kind,
-                                            mfma_iters, direct, s), lib.peaks_last_error, "peaks")
-                torch.cuda.synchronize()
-                t = ticks.cpu().numpy()
-                tile_ns.append(statistics.median(t[:4 * blocks].tolist()) * 10.0 / tiles)
-                if kind:
-                    mt = statistics.median(t[1024:1024 + 8 * blocks].tolist()) * 10.0
-                    mfma_tf.append(blocks * 8 * mfma_iters * 8 * flops_per[kind] / (mt * 1e-9) / 1e12)
-            ns = statistics.median(tile_ns)
-            tf = statistics.median(mfma_tf) if mfma_tf else None
-            row = {"rate": "staging beside MFMA", "mfma": names[kind],
-                   "staging": "direct to LDS" if direct else "through registers",
-                   "ns_per_tile": round(ns, 1), "staging_tbs": round(blocks * 32768 / ns / 1e3, 2),
-                   "mfma_tflops": round(tf, 1) if tf else None}
-            print(json.dumps(row), flush=True)
-            rows.append(row)
-    print("\n| MFMA waves (2 per SIMD) | staging | ns per 32 KB tile pair per CU | staging TB/s "
-          "(chip) | MFMA TFLOP/s |")
-    print("|---|---|---:|---:|---:|")
+    for kind, direct, mw, ns_w in configs:
+        tile_ns, mfma_tf = [], []
+        for _ in range(iters):
+            capi.check(lib.peaks_coexec(P(A), P(B), P(out), P(ticks), blocks, tiles, kind,
+                                        mfma_iters, direct, mw, ns_w, s),
+                       lib.peaks_last_error, "peaks")
+            torch.cuda.synchronize()
+            t = ticks.cpu().numpy()
+            tile_ns.append(statistics.median(t[:ns_w * blocks].tolist()) * 10.0 / tiles)
+            if kind:
+                mt = statistics.median([int(t[2048 + 8 * b + w]) for b in range(blocks)
+                                        for w in range(mw)]) * 10.0
+                mfma_tf.append(blocks * mw * mfma_iters * 8 * flops_per[kind] / (mt * 1e-9) / 1e12)
+        ns = statistics.median(tile_ns)
+        tf = statistics.median(mfma_tf) if mfma_tf else None
+        row = {"rate": "staging beside MFMA", "mfma": names[kind],
+               "mfma_waves_per_simd": mw // 4 if kind else 0, "stagers_per_simd": ns_w // 4,
+               "staging": "direct to LDS" if direct else "through registers",
+               "ns_per_tile": round(ns, 1), "staging_tbs": round(blocks * 32768 / ns / 1e3, 2),
+               "mfma_tflops": round(tf, 1) if tf else None}
+        print(json.dumps(row), flush=True)
+        rows.append(row)
+    print("\n| MFMA | MFMA waves / SIMD | stagers / SIMD | staging | ns per 32 KB tile pair per CU | "
+          "staging TB/s (chip) | MFMA TFLOP/s |")
+    print("|---|---:|---:|---|---:|---:|---:|")
     for r in rows:
-        print(f"| {r['mfma']} | {r['staging']} | {r['ns_per_tile']:,.0f} | {r['staging_tbs']:.2f} | "
+        print(f"| {r['mfma']} | {r['mfma_waves_per_simd']} | {r['stagers_per_simd']} | {r['staging']} | "
+              f"{r['ns_per_tile']:,.0f} | {r['staging_tbs']:.2f} | "
               f"{r['mfma_tflops'] if r['mfma_tflops'] else '-'} |")
+    return 0
+
+
+def joint(iters, tiles=64):
+    """The same MFMA work per SIMD on one or two waves beside a pipelined
+    staging wave (peak_joint_kernel): 64 tile pairs of 32 KB per CU straight
+    into LDS with two or three in flight, and 0-1536 rounds of eight fp32
+    16x16x4 MFMAs per SIMD (1024 rounds = 128 MFMAs per tile pair, the RBF
+    backward's ratio).  Reports the workgroup span and each side's time
+    (median over the CUs, median of `iters` launches)."""
+    import torch
+    dev = torch.device("cuda:0")
+    lib = _lib()
+    s = capi.stream_of(torch.empty(1, device=dev))
+    P = capi.ptr
+    n = 4096
+    A = torch.ones(n * n, device=dev)
+    B = torch.ones(n * n, device=dev)
+    out = torch.zeros(2, device=dev)
+    ticks = torch.zeros(1024, dtype=torch.int64, device=dev)
+    blocks = min(256, torch.cuda.get_device_properties(dev).multi_processor_count)
+    rows = []
+    for depth in (2, 3):
+        for simd_iters in (0, 512, 1024, 1536):
+            for mw, inl in ((((0, 0),) if simd_iters == 0 else ((4, 0), (8, 0), (4, 1)))):
+                span, stg, mf = [], [], []
+                for _ in range(iters):
+                    capi.check(lib.peaks_joint(P(A), P(B), P(out), P(ticks), blocks, tiles,
+                                               simd_iters, mw, depth, inl, s),
+                               lib.peaks_last_error, "peaks")
+                    torch.cuda.synchronize()
+                    t = ticks.cpu().numpy()[:4 * blocks].reshape(blocks, 4)
+                    span.append(statistics.median(t[:, 0].tolist()) / 100.0)
+                    stg.append(statistics.median(t[:, 1].tolist()) / 100.0)
+                    mf.append(statistics.median(t[:, 2].tolist()) / 100.0)
+                row = {"rate": "joint staging + MFMA", "depth": depth, "simd_mfma_rounds": simd_iters,
+                       "mfma_waves_per_simd": mw // 4,
+                       "staged_by": "the MFMA wave" if inl else ("a staging wave" if mw else "-"),
+                       "span_us": round(statistics.median(span), 2),
+                       "staging_us": round(statistics.median(stg), 2),
+                       "mfma_us": round(statistics.median(mf), 2)}
+                print(json.dumps(row), flush=True)
+                rows.append(row)
+    print("\n| tiles in flight | MFMA rounds per SIMD | MFMA waves / SIMD | tiles staged by | "
+          "workgroup span µs | staging µs | MFMA µs |")
+    print("|---:|---:|---:|---|---:|---:|---:|")
+    for r in rows:
+        print(f"| {r['depth']} | {r['simd_mfma_rounds']} | {r['mfma_waves_per_simd']} | "
+              f"{r['staged_by']} | {r['span_us']:.2f} | {r['staging_us']:.2f} | {r['mfma_us']:.2f} |")
     return 0
 
 
@@ -216,6 +272,9 @@ def main(argv=None):
                     help="comma-separated workgroup counts for --sized-copy (default: a sweep)")
     ap.add_argument("--coexec", action="store_true",
                     help="staging waves beside MFMA waves on one CU instead (peak_coexec_kernel)")
+    ap.add_argument("--joint", action="store_true",
+                    help="the same MFMA work on one or two waves per SIMD beside a pipelined "
+                         "staging wave instead (peak_joint_kernel)")
     ns = ap.parse_args(argv)
     import torch
     if not torch.cuda.is_available():
@@ -223,6 +282,8 @@ def main(argv=None):
         return 2
     if ns.coexec:
         return coexec(min(ns.iters, 7))
+    if ns.joint:
+        return joint(min(ns.iters, 7))
     if ns.sized_copy:
         blocks = tuple(int(v) for v in ns.blocks.split(",")) if ns.blocks else None
         return sized_copy([int(v) for v in ns.sized_copy.split(",")], ns.iters, blocks)

@@ -134,14 +134,17 @@ def _wide_spmm_inputs(m=2048, k=16384, d=8, per_row=64, seed=0):
             "vals": torch.randn(m * per_row, generator=g), "X": torch.randn(k, d, generator=g)}
 
 
-@pytest.mark.parametrize("shape", ["reference default M=K=4096 D=64",
-                                   "K=16384 D=8 (80 KB of scatter LDS)"])
+@pytest.mark.parametrize("shape", ["reference default M=K=4096 D=64 (column blocks)",
+                                   "K=16384 D=8 (column blocks of 64)",
+                                   "K=16384 D=32 (column-major copy, 80 KB of scatter LDS)"])
 def test_spmm_backward_graph_replays_with_new_inputs(shape):
+    """Both D > 1 dX routes captured once and replayed on new dY: every
+    replay matches the float64 oracle and an eager call bit for bit."""
     announce(f"spmm backward graph capture ({shape})")
     from cases.spmv import op, reference as ref
     from oracle import spmv as osp
     t = ref.make_inputs(0, torch.float32, "cpu") if shape.startswith("reference") \
-        else _wide_spmm_inputs()
+        else _wide_spmm_inputs(d=int(shape.split("D=")[1].split()[0]))
     ptr, col, vals, X = (t[k].cuda() for k in ("row_ptr", "col_idx", "vals", "X"))
     M, D = ptr.numel() - 1, X.shape[1]
     dy_static = torch.zeros(M, D, device="cuda")
