@@ -23,7 +23,7 @@
 //    registers; reductions are wave64 DPP lane moves (quad_perm and row
 //    mirrors within each 16-lane row, then v_readlane across the four rows)
 //    plus one LDS step across waves.
-//  * Backward: a workgroup walks a contiguous block of rows, prefetching the
+//  * Backward: each of G workgroups walks every G-th row, prefetching the
 //    next row's dy and x while it finishes the current one, and accumulates
 //    its partial dw (/ dbias) in registers.  The per-block partials ([G][D])
 //    are summed by rn_colsum_kernel in one stream-ordered pass, every sum
@@ -179,21 +179,25 @@ __global__ __launch_bounds__(kBlock) void rn_fwd_generic_kernel(
 }
 
 // ----------------------------------------------------------------- backward
-// Level 1: block b handles rows [b*rpb, min(B, (b+1)*rpb)), one row at a
-// time with all 256 threads (V float4 per thread), and writes its partial
-// dw (/ dbias) row to pw[b] (/ pb[b]).
+// Level 1: block b of G handles rows b, b + G, b + 2G, ... in that order,
+// one row at a time with all 256 threads (V float4 per thread), and writes
+// its partial dw (/ dbias) row to pw[b] (/ pb[b]).  The strided row order
+// keeps the G blocks' concurrent reads and writes inside one window of about
+// G consecutive rows of each array; contiguous blocks of rows per block
+// scattered them G row blocks apart and streamed about 10 % slower
+// (72.6 against 65.0 us at 8192 x 4096).
 template <class P, int V, bool FULL>
 __global__ __launch_bounds__(kBlock) void rn_bwd_kernel(
     const float* __restrict__ dy, const float* __restrict__ x,
     const float* __restrict__ w, const float* __restrict__ stat0,
     const float* __restrict__ stat1, float* __restrict__ dx,
-    float* __restrict__ pw, float* __restrict__ pb, int64_t B, int D,
-    int64_t rpb) {
+    float* __restrict__ pw, float* __restrict__ pb, int64_t B, int D) {
   __shared__ float red[8];
   const int t = threadIdx.x;
   const int D4 = D >> 2;
-  const int64_t r0 = (int64_t)blockIdx.x * rpb;
-  const int64_t r1 = min(B, r0 + rpb);
+  const int64_t G = gridDim.x;  // G <= B: every block has a row
+  const int64_t r0 = blockIdx.x;
+  const int64_t rlast = r0 + (B - 1 - r0) / G * G;
   const f32x4* w4 = reinterpret_cast<const f32x4*>(w);
 
   f32x4 wv[V], aw[V], ab[V], gcur[V], xcur[V], gnext[V], xnext[V];
@@ -222,13 +226,13 @@ __global__ __launch_bounds__(kBlock) void rn_bwd_kernel(
       }
     }
   };
-  if (r0 < r1) load_row(r0, gcur, xcur);
+  load_row(r0, gcur, xcur);
   const float inv_d = 1.f / (float)D;
-  for (int64_t r = r0; r < r1; ++r) {
+  for (int64_t r = r0; r < B; r += G) {
     // Unconditional prefetch (the last row re-reads itself): a conditional
     // one makes the number of loads in flight path dependent and the
     // compiler then waits for all of them before using the current row.
-    load_row(min(r + 1, r1 - 1), gnext, xnext);
+    load_row(min(r + G, rlast), gnext, xnext);
     const float mu = P::kCentered ? stat0[r] : 0.f;
     const float rs = P::rs(stat1[r]);
     float sg = 0.f, sgx = 0.f;
@@ -403,7 +407,7 @@ struct Plan {
   int tpr = 256;        // forward threads per row
   int v = 4;            // float4 per thread
   int64_t G = 0;        // partial rows of dw / dbias
-  int64_t rpb = 0;      // rows per block: backward blocks (cached) or partial groups (generic)
+  int64_t rpb = 0;      // rows per backward block (cached; rows strided by G) or partial group (generic)
 };
 
 inline Plan plan(int64_t B, int64_t D, bool aligned) {
@@ -507,10 +511,10 @@ int run_backward(const float* dy, const float* x, const float* w, const float* s
   do {                                                                                       \
     if (D / 4 == 256 * (V))                                                                  \
       hipLaunchKernelGGL((rn_bwd_kernel<P, V, true>), dim3((unsigned)p.G), dim3(kBlock), 0,  \
-                         stream, dy, x, w, stat0, stat1, dx, pw, pb, B, (int)D, p.rpb);      \
+                         stream, dy, x, w, stat0, stat1, dx, pw, pb, B, (int)D);             \
     else                                                                                     \
       hipLaunchKernelGGL((rn_bwd_kernel<P, V, false>), dim3((unsigned)p.G), dim3(kBlock), 0, \
-                         stream, dy, x, w, stat0, stat1, dx, pw, pb, B, (int)D, p.rpb);      \
+                         stream, dy, x, w, stat0, stat1, dx, pw, pb, B, (int)D);             \
   } while (0)
     const int64_t d4 = D / 4;
     if (d4 <= 256) RN_BWD(1);
