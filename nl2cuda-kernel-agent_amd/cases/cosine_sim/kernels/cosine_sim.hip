@@ -264,9 +264,10 @@ int cosine_sim_forward_f32(const float* A, const float* B, float* S, float* inv_
   if (D == kD && nl2k::aligned16(A) && nl2k::aligned16(B) &&
       nl2k::pairwise::plan_forward(N, M, fp)) {
     const int vec_store = (M % 4 == 0) && nl2k::aligned16(S);
-    hipLaunchKernelGGL(nl2k::pairwise::pair_fwd_d64_kernel<CosFwdOp>, dim3(fp.n_wg), dim3(256),
-                       0, stream, A, B, S, (int)N, (int)M, CosFwdOp{eps}, fp.n_jt, fp.n_units,
-                       fp.upw, vec_store, inv_a, inv_b);
+    auto* kernel = fp.ib == 2 ? &nl2k::pairwise::pair_fwd_d64_kernel<CosFwdOp, 2>
+                              : &nl2k::pairwise::pair_fwd_d64_kernel<CosFwdOp, 4>;
+    hipLaunchKernelGGL(kernel, dim3(fp.n_wg), dim3(256), 0, stream, A, B, S, (int)N, (int)M,
+                       CosFwdOp{eps}, fp.n_jt, fp.n_units, fp.upw, vec_store, inv_a, inv_b);
     return nl2k::check_launch(who);
   }
   st = launch_norms(A, inv_a, N, D, eps, stream);

@@ -300,9 +300,11 @@ int rbf_forward_f32(const float* X, const float* Y, float* K, int64_t N,
   if (D == kD && nl2k::aligned16(X) && nl2k::aligned16(Y) &&
       nl2k::pairwise::plan_forward(N, M, fp)) {
     const int vec_store = (M % 4 == 0) && nl2k::aligned16(K);
-    hipLaunchKernelGGL(nl2k::pairwise::pair_fwd_d64_kernel<RbfFwdOp>, dim3(fp.n_wg), dim3(256),
-                       0, stream, X, Y, K, (int)N, (int)M, RbfFwdOp{-gamma * kLog2e}, fp.n_jt,
-                       fp.n_units, fp.upw, vec_store, nullptr, nullptr);
+    auto* kernel = fp.ib == 2 ? &nl2k::pairwise::pair_fwd_d64_kernel<RbfFwdOp, 2>
+                              : &nl2k::pairwise::pair_fwd_d64_kernel<RbfFwdOp, 4>;
+    hipLaunchKernelGGL(kernel, dim3(fp.n_wg), dim3(256), 0, stream, X, Y, K, (int)N, (int)M,
+                       RbfFwdOp{-gamma * kLog2e}, fp.n_jt, fp.n_units, fp.upw, vec_store, nullptr,
+                       nullptr);
     return nl2k::check_launch("rbf_forward_f32");
   }
   const int64_t total = N * M;

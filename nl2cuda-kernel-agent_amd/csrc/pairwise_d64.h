@@ -2,8 +2,8 @@
 // (gfx950): the tile engines behind the RBF and cosine-similarity cases.
 //
 //  * pair_fwd_d64_kernel<Op>: out[i,j] = Op::out(x_i . y_j, row term i,
-//    column term j) for X [N,64], Y [M,64].  Work unit = 256 rows x 64
-//    columns; a workgroup of four waves walks a contiguous range of units.
+//    column term j) for X [N,64], Y [M,64].  Work unit = 256 (or 128) rows x
+//    64 columns; a workgroup of four waves walks a contiguous range of units.
 //    Each wave keeps its 64 X rows in MFMA operand registers (v_mfma_f32_
 //    16x16x4_f32 layout, contraction index k = 16q + 4h + u permuted the same
 //    way for both operands so every lane moves 16 contiguous bytes per load)
@@ -39,7 +39,7 @@ constexpr int kLds = 68;         // padded LDS row stride (floats)
 constexpr int kTileFloats = kTile * kLds;
 constexpr int kTargetRegions = 256;  // one backward workgroup per CU
 constexpr int kFwdWorkgroups = 512;  // two forward workgroups per CU
-constexpr int kFwdRows = 256;        // rows per forward unit (4 waves x 64)
+constexpr int kFwdRows = 256;        // rows per forward unit (4 waves x 64), or 128 (see plan_forward)
 // The tile kernels index rows and columns with int, up to a tile or region
 // past the last one; larger N or M take the callers' generic (int64) kernels.
 constexpr int64_t kMaxTileDim = INT32_MAX - 1024;
@@ -55,7 +55,8 @@ constexpr int64_t kMaxTileDim = INT32_MAX - 1024;
 //                                       row's epilogue term
 //   float col(f32x4& y, float sy)       Y row prep at staging (y: 4 values)
 //   float out(float dot, float rt, float ct)  the output entry
-template <class Op>
+// IB: 16-row blocks per wave (4: 256-row units, 2: 128-row units).
+template <class Op, int IB>
 __global__ __launch_bounds__(256, 2) void pair_fwd_d64_kernel(
     const float* __restrict__ X, const float* __restrict__ Y,
     float* __restrict__ K, int N, int M, Op op, int n_jt,
@@ -69,8 +70,13 @@ __global__ __launch_bounds__(256, 2) void pair_fwd_d64_kernel(
   const int wave = tid >> 6;
   const int n = lane & 15;
   const int h = lane >> 4;
-  const int u_begin = blockIdx.x * units_per_wg;
-  const int u_end = min(u_begin + units_per_wg, n_units);
+  // Workgroup b takes units_per_wg units, or one more for the first
+  // n_units - units_per_wg * gridDim.x workgroups (no division here: a
+  // 64-bit one on every workgroup's critical path cost about 1 us).
+  const int extra = n_units - units_per_wg * (int)gridDim.x;
+  const int bx = (int)blockIdx.x;
+  const int u_begin = bx * units_per_wg + min(bx, extra);
+  const int u_end = min(u_begin + units_per_wg + (bx < extra ? 1 : 0), n_units);
   if (u_begin >= u_end) return;  // workgroup-uniform
 
   // Y staging: thread t moves float4 (row (t >> 4) + 16 s, cols 4 (t & 15)..).
@@ -103,15 +109,16 @@ __global__ __launch_bounds__(256, 2) void pair_fwd_d64_kernel(
   // 16 ib + n of this wave's strip.  Contraction step (q, u) uses k-slot h.
   // The loads go out q-major, so the first contraction steps wait only for
   // their own slices.
-  f32x4 xb[4][4];
-  float ax[4];  // Op::row term of row 16 ib + n
+  constexpr int kRows = 64 * IB;  // rows per unit
+  f32x4 xb[IB][4];
+  float ax[IB];  // Op::row term of row 16 ib + n
   int cur_rb = -1;
   auto load_x = [&](int rb) {
-    const int i0 = rb * kFwdRows + wave * 64;
+    const int i0 = rb * kRows + wave * 16 * IB;
 #pragma unroll
     for (int q = 0; q < 4; ++q)
 #pragma unroll
-      for (int ib = 0; ib < 4; ++ib) {
+      for (int ib = 0; ib < IB; ++ib) {
         const int ir = min(i0 + ib * 16 + n, N - 1);
         xb[ib][q] = load4(X + (size_t)ir * kD + 16 * q + 4 * h);
       }
@@ -119,7 +126,7 @@ __global__ __launch_bounds__(256, 2) void pair_fwd_d64_kernel(
   };
   auto row_terms = [&]() {
 #pragma unroll
-    for (int ib = 0; ib < 4; ++ib) {
+    for (int ib = 0; ib < IB; ++ib) {
       float sx = 0.f;
 #pragma unroll
       for (int q = 0; q < 4; ++q)
@@ -149,11 +156,11 @@ __global__ __launch_bounds__(256, 2) void pair_fwd_d64_kernel(
     __builtin_amdgcn_sched_barrier(0);
 
     const float* Yb = Ys[buf];
-    f32x4 acc[4][4];
+    f32x4 acc[4][IB];
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
-      for (int b = 0; b < 4; ++b) acc[a][b] = zero4();
+      for (int b = 0; b < IB; ++b) acc[a][b] = zero4();
     // A operands (Y rows 16 jb + n, k = 16q + 4h .. +3), read one q ahead.
     f32x4 ya[2][4];
 #pragma unroll
@@ -171,7 +178,7 @@ __global__ __launch_bounds__(256, 2) void pair_fwd_d64_kernel(
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
-          for (int ib = 0; ib < 4; ++ib)
+          for (int ib = 0; ib < IB; ++ib)
             acc[jb][ib] = mfma16x4(ya[q & 1][jb][uu], xb[ib][q][uu], acc[jb][ib]);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -181,25 +188,25 @@ __global__ __launch_bounds__(256, 2) void pair_fwd_d64_kernel(
       terms_due = false;
     }
     // Epilogue: out[i][j..j+3], i = i0 + 16 ib + n, j = j0 + 16 jb + 4h.
-    const int i0 = (u / n_jt) * kFwdRows + wave * 64;
+    const int i0 = (u / n_jt) * kRows + wave * 16 * IB;
     const int j0 = (u % n_jt) * kTile;
     if constexpr (Op::kSideOut) {
       // Row terms once per row block (its column tile 0), column terms once
       // per column tile (row block 0).
       if (u % n_jt == 0 && h == 0) {
 #pragma unroll
-        for (int ib = 0; ib < 4; ++ib)
+        for (int ib = 0; ib < IB; ++ib)
           if (i0 + ib * 16 + n < N) rowv[i0 + ib * 16 + n] = ax[ib];
       }
       if (u / n_jt == 0 && tid < kTile && j0 + tid < M) colv[j0 + tid] = nyS[buf][tid];
     }
-    const bool full = vec_store && i0 + 64 <= N && j0 + 64 <= M;
+    const bool full = vec_store && i0 + 16 * IB <= N && j0 + 64 <= M;
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb) {
       const f32x4 ny = load4(&nyS[buf][jb * 16 + 4 * h]);
       const int j = j0 + jb * 16 + 4 * h;
 #pragma unroll
-      for (int ib = 0; ib < 4; ++ib) {
+      for (int ib = 0; ib < IB; ++ib) {
         const int i = i0 + ib * 16 + n;
         f32x4 o;
 #pragma unroll
@@ -230,20 +237,28 @@ __global__ __launch_bounds__(256, 2) void pair_fwd_d64_kernel(
   }
 }
 
-// Launch shape of the forward: units of 256 x 64, at most kFwdWorkgroups
-// workgroups, each taking a contiguous range of units.
+// Launch shape of the forward: units of 256 x 64 (ib = 4 row blocks of 16
+// per wave) or 128 x 64 (ib = 2), spread over at most kFwdWorkgroups
+// workgroups (two per CU) as evenly as whole units allow, each workgroup
+// taking a contiguous range.  128-row units when 256-row ones would give
+// fewer than two per workgroup, so the grid stays full and balanced (with
+// identical bits): 14.5 against 15.2 us at 2048 x 2048, 24.5 against
+// 32.2 us at 3000 x 3000, 9.6 against 12.3 at 1024 x 1024; an even spread
+// instead of ceil(units / 512) per workgroup: 49.1 against 54.0 us at
+// 5000 x 5000, 60.3 against 65.4 at 6000 x 6000.
 struct FwdPlan {
-  int n_jt = 0, n_units = 0, upw = 0, n_wg = 0;
+  int ib = 4, n_jt = 0, n_units = 0, upw = 0, n_wg = 0;
 };
 
 inline bool plan_forward(int64_t N, int64_t M, FwdPlan& p) {
   if (N > kMaxTileDim || M > kMaxTileDim) return false;
   p.n_jt = (int)ceil_div(M, kTile);
-  const int64_t n_units64 = ceil_div(N, kFwdRows) * p.n_jt;
+  p.ib = ceil_div(N, kFwdRows) * p.n_jt < 2 * kFwdWorkgroups ? 2 : 4;
+  const int64_t n_units64 = ceil_div(N, 64 * p.ib) * p.n_jt;
   if (n_units64 > INT32_MAX) return false;
   p.n_units = (int)n_units64;
-  p.upw = (int)ceil_div(p.n_units, kFwdWorkgroups);
-  p.n_wg = (int)ceil_div(p.n_units, p.upw);
+  p.n_wg = (int)std::min<int64_t>(p.n_units, kFwdWorkgroups);
+  p.upw = p.n_units / p.n_wg;  // n_units % n_wg workgroups take one more
   return true;
 }
 
@@ -987,12 +1002,27 @@ inline BwdPlan plan_backward(int64_t N, int64_t M, int64_t D, bool sums) {
   if (D != kD || N <= 0 || M <= 0 || N > kMaxTileDim || M > kMaxTileDim) return p;
   p.fast = true;
   // Region edges above 256 would need more than 256 accumulator registers
-  // per lane on the dY side (two waves per SIMD), so R stays <= 256.
+  // per lane on the dY side (two waves per SIMD), so R stays <= 256.  The
+  // edge is the one with the lowest modelled time, in units of one 64 x 64
+  // tile step (~2.35 us): one workgroup runs per CU at a time, so a launch
+  // takes ceil(regions / 256) rounds of (R / 64)^2 steps plus about four
+  // steps of fill and drain each, and the reduce moves the partial rows
+  // (written once, read once) at about kStepBytes per step.  Measured
+  // against the earlier rule (the largest edge giving >= 256 regions):
+  // backward 44.7 against 64.3 us at 3000^2 (edge 192), 61.1 against
+  // 78.6 at 3500^2 (256), 148.1 against 160.7 at 6000^2 (192), 26.1
+  // against 32.7 at 1500^2 (128); 2048^2, 4096^2 and 8192^2 keep their edges.
+  constexpr double kStepBytes = 11.75e6;
   int R = 64;
-  for (int cand = 256; cand >= 64; cand >>= 1) {
-    if (ceil_div(N, cand) * ceil_div(M, cand) >= kTargetRegions) {
+  double best = 0.0;
+  for (int cand : {256, 192, 128, 64}) {
+    const int64_t jc = cand / kTile, nri = ceil_div(N, cand), nrj = ceil_div(M, cand);
+    const int64_t rounds = ceil_div(nri * nrj, kTargetRegions);
+    const double partial_bytes = (double)(nrj * N + nri * M) * (kD + 1) * sizeof(float) * 2;
+    const double cost = (double)(rounds * (jc * jc + 4)) + partial_bytes / kStepBytes;
+    if (cand == 256 || cost < best) {
+      best = cost;
       R = cand;
-      break;
     }
   }
   p.R = R;
@@ -1046,6 +1076,7 @@ void launch_bwd_tiles(const BwdPlan& p, const float* X, const float* Y, const fl
   switch (p.JC) {
     case 1: launch_bwd_tiles<Op, 1>(p, X, Y, dK, K, ws, N, M, vec_nm, sx, sy, stream); break;
     case 2: launch_bwd_tiles<Op, 2>(p, X, Y, dK, K, ws, N, M, vec_nm, sx, sy, stream); break;
+    case 3: launch_bwd_tiles<Op, 3>(p, X, Y, dK, K, ws, N, M, vec_nm, sx, sy, stream); break;
     default: launch_bwd_tiles<Op, 4>(p, X, Y, dK, K, ws, N, M, vec_nm, sx, sy, stream); break;
   }
 }

@@ -76,7 +76,7 @@ def test_cosine_square_vs_oracle(n, seed):
 
 
 @pytest.mark.parametrize("n,m,d", [(1000, 3000, 64), (1, 1, 64), (5, 7, 64), (300, 257, 64),
-                                   (129, 65, 32), (200, 150, 100), (64, 64, 1)])
+                                   (129, 65, 32), (200, 150, 100), (64, 64, 1), (3000, 3008, 64)])
 def test_cosine_shapes(n, m, d):
     announce(f"cosine_sim N={n} M={m} D={d}")
     A, B, dS = _inputs(n, m, d, n + m + d)

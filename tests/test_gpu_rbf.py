@@ -99,7 +99,10 @@ def test_rbf_8192_parity_and_identities(seed):
                                  (128, 4100), (1000, 999), (513, 2049),
                                  # multiples of 64: the full-tile (buffer-load) backward
                                  # at every region width, square and not
-                                 (64, 192), (256, 640), (1088, 960), (3072, 1024)])
+                                 (64, 192), (256, 640), (1088, 960), (3072, 1024),
+                                 # 192-wide regions (ragged, full tiles, scalar loads, two
+                                 # rounds); forward units spread unevenly, 128 or 256 rows
+                                 (3000, 3000), (3008, 2944), (2999, 3001), (5000, 5000)])
 def test_rbf_ragged_shapes(n, m):
     announce(f"rbf ragged n={n} m={m}")
     _check_full(*_inputs(n, m, 64, n + m), 0.5)

@@ -72,7 +72,8 @@ def test_noalloc_backward_rejects_a_shape_beyond_its_scratch():
 def test_noalloc_backward_generic_path_needs_no_scratch():
     """A misaligned X takes the generic kernels, which use no scratch: the
     no-alloc entry runs it even where the tile path's partials would not fit
-    (N = M = 6000 needs 75 MB of them), bit-identical to the workspace entry."""
+    (N = M = 6000 needs about 100 MB of them), bit-identical to the workspace
+    entry."""
     n = m = 6000
     announce(f"rbf noalloc, misaligned X, n={n} m={m} (generic kernels)")
     from cases.rbf import op
