@@ -121,6 +121,7 @@ inline int resident_blocks(const void* kernel, int threads, int* out) {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef double f64x2 __attribute__((ext_vector_type(2)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ f32x4 load4(const float* p) {
   return *reinterpret_cast<const f32x4*>(p);
@@ -146,6 +147,14 @@ __device__ __forceinline__ buffer_rsrc make_rsrc(const void* base, uint32_t byte
 
 __device__ __forceinline__ f32x4 buffer_load4(buffer_rsrc r, uint32_t lane_off, int wave_off) {
   return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, lane_off, wave_off, 0));
+}
+
+// Store through a raw buffer resource: a lane whose offset is at or past the
+// resource's `bytes` writes nothing, so a store that only some lanes (or, with
+// bytes = 0, no lane) may make is still one unconditional instruction.
+__device__ __forceinline__ void buffer_store4(buffer_rsrc r, f32x4 v, uint32_t lane_off,
+                                              int wave_off) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, lane_off, wave_off, 0);
 }
 
 // One 16x16x4 fp32 MFMA: acc[m][n] += sum_k A[m][k] * B[k][n].

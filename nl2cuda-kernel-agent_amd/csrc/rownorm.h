@@ -23,9 +23,11 @@
 //    registers; reductions are wave64 DPP lane moves (quad_perm and row
 //    mirrors within each 16-lane row, then v_readlane across the four rows)
 //    plus one LDS step across waves.
-//  * Backward: each of G workgroups walks every G-th row, prefetching the
-//    next row's dy and x while it finishes the current one, and accumulates
-//    its partial dw (/ dbias) in registers.  The per-block partials ([G][D])
+//  * Backward: each of G workgroups holds H = 1 or 2 independent 256-thread
+//    halves; half h of block b walks rows b + h G, every H G-th row after it,
+//    prefetching the next row's dy and x while it finishes the current one,
+//    and accumulates its partial dw (/ dbias) in registers; the block adds
+//    its halves' partials in LDS and writes one partial row.  The per-block partials ([G][D])
 //    are summed by rn_colsum_kernel in one stream-ordered pass, every sum
 //    in a fixed order, so dw and dbias are deterministic.
 //  * Any other shape uses generic kernels that re-read x: one workgroup per
@@ -54,13 +56,14 @@ __device__ __forceinline__ float dot4(f32x4 a, f32x4 b) {
 __device__ __forceinline__ float hsum4(f32x4 a) { return (a[0] + a[1]) + (a[2] + a[3]); }
 
 // Sum over the TPR threads that share a row (TPR = 64 or 256), result in all
-// of them.  `red` is a per-block LDS scratch of at least 2 * 4 floats.
+// of them.  `red` is LDS scratch of at least 2 * 4 floats per row group; with
+// TPR = 256 every thread of the block must take part (it holds barriers).
 template <int TPR>
 __device__ __forceinline__ void row_sum2(float& a, float& b, float* red) {
   a = wave_sum_dpp(a);
   b = wave_sum_dpp(b);
   if (TPR == 256) {
-    const int wave = threadIdx.x >> 6;
+    const int wave = (threadIdx.x >> 6) & 3;  // the wave within the row's 256 threads
     __syncthreads();  // red may still be read from the previous use
     if ((threadIdx.x & 63) == 0) {
       red[wave] = a;
@@ -98,7 +101,10 @@ __global__ __launch_bounds__(kBlock) void rn_fwd_kernel(
   __shared__ float red[8];
   constexpr int RPB = kBlock / TPR;
   const int64_t S = (int64_t)gridDim.x * RPB;
-  const int64_t r0 = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;
+  // The row group is wave uniform: from lane 0, so rows and row pointers
+  // stay scalar (buffer resources need them so).
+  const int64_t r0 =
+      (int64_t)blockIdx.x * RPB + __builtin_amdgcn_readfirstlane((int)threadIdx.x) / TPR;
   const int t = threadIdx.x % TPR;
   const int D4 = D >> 2;
   // TPR = 256: the grid has at most B blocks, so a whole block walks the
@@ -109,17 +115,17 @@ __global__ __launch_bounds__(kBlock) void rn_fwd_kernel(
   const f32x4* w4 = reinterpret_cast<const f32x4*>(w);
   const f32x4* b4 = reinterpret_cast<const f32x4*>(bias);
   f32x4 wv[V], bv[V], cur[V], nxt[V];
+  // Ragged rows (not FULL) load and store through a buffer resource over
+  // the row: lanes past its end read zeros and write nothing, with no
+  // branch, so the count of memory operations in flight stays the same on
+  // every path and the loop waits only for the loads it uses.
   auto load_row = [&](int64_t r, f32x4 (&v)[V]) {
     const f32x4* xr = reinterpret_cast<const f32x4*>(x + r * D);
+    const buffer_rsrc rx = make_rsrc(x + r * D, (uint32_t)D * 4u);
 #pragma unroll
     for (int k = 0; k < V; ++k) {
       const int c = t + k * TPR;
-      if (FULL) {
-        v[k] = xr[c];
-      } else {
-        const f32x4 val = xr[min(c, D4 - 1)];
-        v[k] = c < D4 ? val : zero4();
-      }
+      v[k] = FULL ? xr[c] : buffer_load4(rx, (uint32_t)c * 16u, 0);
     }
   };
   load_row(r0, cur);
@@ -157,15 +163,16 @@ __global__ __launch_bounds__(kBlock) void rn_fwd_kernel(
       stat1[r] = P::stat1(rs, ss);
     }
     f32x4* yr = reinterpret_cast<f32x4*>(y + r * D);
+    const buffer_rsrc ry = make_rsrc(y + r * D, (uint32_t)D * 4u);
 #pragma unroll
     for (int k = 0; k < V; ++k) {
       const int c = t + k * TPR;
-      if (FULL || c < D4) {
-        if constexpr (P::kBias)
-          yr[c] = (cur[k] - mu) * rs * wv[k] + bv[k];
-        else
-          yr[c] = (cur[k] - mu) * rs * wv[k];
-      }
+      f32x4 yv = (cur[k] - mu) * rs * wv[k];
+      if constexpr (P::kBias) yv += bv[k];
+      if (FULL)
+        yr[c] = yv;
+      else
+        buffer_store4(ry, yv, (uint32_t)c * 16u, 0);
     }
 #pragma unroll
     for (int k = 0; k < V; ++k) cur[k] = nxt[k];
@@ -207,25 +214,45 @@ __global__ __launch_bounds__(kBlock) void rn_fwd_generic_kernel(
 }
 
 // ----------------------------------------------------------------- backward
-// Level 1: block b of G handles rows b, b + G, b + 2G, ... in that order,
-// one row at a time with all 256 threads (V float4 per thread), and writes
-// its partial dw (/ dbias) row to pw[b] (/ pb[b]).  The strided row order
-// keeps the G blocks' concurrent reads and writes inside one window of about
-// G consecutive rows of each array; contiguous blocks of rows per block
-// scattered them G row blocks apart and streamed about 10 % slower
-// (72.6 against 65.0 us at 8192 x 4096).
-template <class P, int V, bool FULL>
-__global__ __launch_bounds__(kBlock) void rn_bwd_kernel(
+// Level 1: block b of G is H halves of 256 threads (V float4 per thread);
+// half h walks rows b + h G, b + h G + S, b + h G + 2S, ... (S = H G rows per
+// sweep), one row at a time, and the block writes the sum of its halves'
+// partial dw (/ dbias) rows (half 0 + half 1, in that order) to pw[b]
+// (/ pb[b]).  Both halves take the same number of steps, half 0's row count,
+// so they pass the same barriers; a half whose row lies past the end runs
+// the step on a clamped row and keeps nothing of it.
+//  * The strided row order keeps the concurrent reads and writes of all
+//    blocks inside one window of about S consecutive rows of each array;
+//    contiguous blocks of rows per block scattered them G row blocks apart
+//    and streamed about 10 % slower (72.6 against 65.0 us at 8192 x 4096).
+//  * Two halves per block (V = 2 and 4) halve the partial rows for the same
+//    waves per SIMD: whole backward 70.3 against 71.8 us at 8192 x 4096,
+//    42.5 against 45.3 at 8192 x 2048.  At V = 1 the rows are short enough
+//    that eight waves meeting at every row's barrier cost more than the
+//    partial rows save (54.3 against 46.3 us at 16384 x 1024); at V = 8 one
+//    half needs more registers than two waves per SIMD allow.
+template <class P, int V, bool FULL, int H>
+__global__ __launch_bounds__(kBlock * H) void rn_bwd_kernel(
     const float* __restrict__ dy, const float* __restrict__ x,
     const float* __restrict__ w, const float* __restrict__ stat0,
     const float* __restrict__ stat1, float* __restrict__ dx,
     float* __restrict__ pw, float* __restrict__ pb, int64_t B, int D) {
-  __shared__ float red[8];
-  const int t = threadIdx.x;
+  static_assert(H == 1 || H == 2, "one or two halves");
+  __shared__ float red[8 * H];
+  constexpr int kParts = P::kBias ? 2 : 1;
+  __shared__ f32x4 s_part[H > 1 ? kParts * kBlock * V : 1];  // half 1's partial rows
+  // The half is wave uniform: take it from lane 0 so that rows, row
+  // pointers and the row predicate stay scalar.
+  const int hf = H > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x) / kBlock : 0;
+  const int t = threadIdx.x % kBlock;
   const int D4 = D >> 2;
-  const int64_t G = gridDim.x;  // G <= B: every block has a row
-  const int64_t r0 = blockIdx.x;
-  const int64_t rlast = r0 + (B - 1 - r0) / G * G;
+  const int64_t G = gridDim.x;  // G <= B: every block's half 0 has a row
+  const int64_t S = (int64_t)H * G;
+  const int64_t r0 = (int64_t)blockIdx.x + hf * G;
+  const int64_t nk = (B - 1 - (int64_t)blockIdx.x) / S + 1;  // steps: half 0's rows
+  // This half's last row (B - 1 for a half with no row at all): the row the
+  // prefetch is clamped to, so the last step re-reads a row it already has.
+  const int64_t rlast = r0 < B ? r0 + (B - 1 - r0) / S * S : B - 1;
   const f32x4* w4 = reinterpret_cast<const f32x4*>(w);
 
   f32x4 wv[V], aw[V], ab[V], gcur[V], xcur[V], gnext[V], xnext[V];
@@ -237,61 +264,89 @@ __global__ __launch_bounds__(kBlock) void rn_bwd_kernel(
     aw[k] = zero4();
     ab[k] = zero4();
   }
+  // Ragged rows load through buffer resources (zeros past the row's end,
+  // no branch; see the store below).
   auto load_row = [&](int64_t r, f32x4 (&g)[V], f32x4 (&xv)[V]) {
     const f32x4* dyr = reinterpret_cast<const f32x4*>(dy + r * D);
     const f32x4* xr = reinterpret_cast<const f32x4*>(x + r * D);
+    const buffer_rsrc rg = make_rsrc(dy + r * D, (uint32_t)D * 4u);
+    const buffer_rsrc rx = make_rsrc(x + r * D, (uint32_t)D * 4u);
 #pragma unroll
     for (int k = 0; k < V; ++k) {
       const int c = t + k * kBlock;
-      if (FULL) {
-        g[k] = dyr[c];
-        xv[k] = xr[c];
-      } else {
-        const int cc = min(c, D4 - 1);
-        const f32x4 a = dyr[cc], b = xr[cc];
-        g[k] = c < D4 ? a : zero4();
-        xv[k] = c < D4 ? b : zero4();
-      }
+      g[k] = FULL ? dyr[c] : buffer_load4(rg, (uint32_t)c * 16u, 0);
+      xv[k] = FULL ? xr[c] : buffer_load4(rx, (uint32_t)c * 16u, 0);
     }
   };
-  load_row(r0, gcur, xcur);
+  load_row(min(r0, rlast), gcur, xcur);
   const float inv_d = 1.f / (float)D;
-  for (int64_t r = r0; r < B; r += G) {
+  int64_t r = r0;
+  for (int64_t k = 0; k < nk; ++k, r += S) {
+    const bool has = H == 1 || r < B;  // false only on half 1's extra step
+    const int64_t rr = has ? r : B - 1;
     // Unconditional prefetch (the last row re-reads itself): a conditional
     // one makes the number of loads in flight path dependent and the
     // compiler then waits for all of them before using the current row.
-    load_row(min(r + G, rlast), gnext, xnext);
-    const float mu = P::kCentered ? stat0[r] : 0.f;
-    const float rs = P::rs(stat1[r]);
+    load_row(min(r + S, rlast), gnext, xnext);
+    const float mu = P::kCentered ? stat0[rr] : 0.f;
+    const float rs = P::rs(stat1[rr]);
     float sg = 0.f, sgx = 0.f;
     f32x4 xh[V];
 #pragma unroll
-    for (int k = 0; k < V; ++k) {
-      xh[k] = (xcur[k] - mu) * rs;
-      const f32x4 g = gcur[k] * wv[k];
+    for (int k2 = 0; k2 < V; ++k2) {
+      xh[k2] = (xcur[k2] - mu) * rs;
+      const f32x4 g = gcur[k2] * wv[k2];
       if constexpr (P::kCentered) sg += hsum4(g);
-      sgx += dot4(g, xh[k]);
-      aw[k] += gcur[k] * xh[k];
-      if constexpr (P::kBias) ab[k] += gcur[k];
+      sgx += dot4(g, xh[k2]);
+    }
+    if (has) {
+#pragma unroll
+      for (int k2 = 0; k2 < V; ++k2) {
+        aw[k2] += gcur[k2] * xh[k2];
+        if constexpr (P::kBias) ab[k2] += gcur[k2];
+      }
     }
     float mg = 0.f, mgx;
     if constexpr (P::kCentered) {
-      row_sum2<kBlock>(sg, sgx, red);
+      row_sum2<kBlock>(sg, sgx, red + 8 * hf);
       mg = sg * inv_d;
       mgx = sgx * inv_d;
     } else {
-      mgx = row_sum1<kBlock>(sgx, red);
+      mgx = row_sum1<kBlock>(sgx, red + 8 * hf);
     }
-    f32x4* dxr = reinterpret_cast<f32x4*>(dx + r * D);
+    {
+      // One unconditional store per float4: the resource spans the row (none
+      // of it without a row), so the column tail and a half's missing row
+      // write nothing.  A store under a branch would make the count of
+      // memory operations in flight path dependent, and the compiler then
+      // waits for this row's stores before it uses the next row's loads.
+      const buffer_rsrc rdx = make_rsrc(dx + rr * D, has ? (uint32_t)D * 4u : 0u);
+#pragma unroll
+      for (int k2 = 0; k2 < V; ++k2) {
+        const int c = t + k2 * kBlock;
+        buffer_store4(rdx, rs * (gcur[k2] * wv[k2] - mg - xh[k2] * mgx), (uint32_t)c * 16u, 0);
+      }
+    }
+#pragma unroll
+    for (int k2 = 0; k2 < V; ++k2) {
+      gcur[k2] = gnext[k2];
+      xcur[k2] = xnext[k2];
+    }
+  }
+  if constexpr (H > 1) {
+    if (hf == 1) {
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        s_part[t + k * kBlock] = aw[k];
+        if constexpr (P::kBias) s_part[kBlock * V + t + k * kBlock] = ab[k];
+      }
+    }
+    __syncthreads();
+    if (hf == 1) return;
 #pragma unroll
     for (int k = 0; k < V; ++k) {
-      const int c = t + k * kBlock;
-      if (FULL || c < D4) dxr[c] = rs * (gcur[k] * wv[k] - mg - xh[k] * mgx);
-    }
-#pragma unroll
-    for (int k = 0; k < V; ++k) {
-      gcur[k] = gnext[k];
-      xcur[k] = xnext[k];
+      aw[k] += s_part[t + k * kBlock];
+      if constexpr (P::kBias) ab[k] += s_part[kBlock * V + t + k * kBlock];
     }
   }
   f32x4* pw4 = reinterpret_cast<f32x4*>(pw + (int64_t)blockIdx.x * D);
@@ -434,8 +489,9 @@ struct Plan {
   bool cached = false;  // row-cached vector path
   int tpr = 256;        // forward threads per row
   int v = 4;            // float4 per thread
+  int halves = 1;       // 256-thread halves per backward block (cached path)
   int64_t G = 0;        // partial rows of dw / dbias
-  int64_t rpb = 0;      // rows per backward block (cached; rows strided by G) or partial group (generic)
+  int64_t rpb = 0;      // cached: rows per backward block before halving (sets G); generic: rows per partial group
 };
 
 inline Plan plan(int64_t B, int64_t D, bool aligned) {
@@ -463,6 +519,10 @@ inline Plan plan(int64_t B, int64_t D, bool aligned) {
     p.rpb = std::max<int64_t>(1, ceil_div(B, s1));
   }
   p.G = B > 0 ? ceil_div(B, p.rpb) : 0;
+  if (p.cached && D / 4 > 256 && D / 4 <= 1024) {  // two halves per block (V = 2, 4)
+    p.halves = 2;
+    p.G = ceil_div(p.G, 2);
+  }
   return p;
 }
 
@@ -535,20 +595,22 @@ int run_backward(const float* dy, const float* x, const float* w, const float* s
   float* pb = pw + p.G * D;
   int st;
   if (p.cached) {
-#define RN_BWD(V)                                                                            \
-  do {                                                                                       \
-    if (D / 4 == 256 * (V))                                                                  \
-      hipLaunchKernelGGL((rn_bwd_kernel<P, V, true>), dim3((unsigned)p.G), dim3(kBlock), 0,  \
-                         stream, dy, x, w, stat0, stat1, dx, pw, pb, B, (int)D);             \
-    else                                                                                     \
-      hipLaunchKernelGGL((rn_bwd_kernel<P, V, false>), dim3((unsigned)p.G), dim3(kBlock), 0, \
-                         stream, dy, x, w, stat0, stat1, dx, pw, pb, B, (int)D);             \
+#define RN_BWD(V, H)                                                                          \
+  do {                                                                                        \
+    if (D / 4 == 256 * (V))                                                                   \
+      hipLaunchKernelGGL((rn_bwd_kernel<P, V, true, H>), dim3((unsigned)p.G),                 \
+                         dim3(kBlock * (H)), 0, stream, dy, x, w, stat0, stat1, dx, pw, pb, B, \
+                         (int)D);                                                             \
+    else                                                                                      \
+      hipLaunchKernelGGL((rn_bwd_kernel<P, V, false, H>), dim3((unsigned)p.G),                \
+                         dim3(kBlock * (H)), 0, stream, dy, x, w, stat0, stat1, dx, pw, pb, B, \
+                         (int)D);                                                             \
   } while (0)
     const int64_t d4 = D / 4;
-    if (d4 <= 256) RN_BWD(1);
-    else if (d4 <= 512) RN_BWD(2);
-    else if (d4 <= 1024) RN_BWD(4);
-    else RN_BWD(8);
+    if (d4 <= 256) RN_BWD(1, 1);
+    else if (d4 <= 512) RN_BWD(2, 2);
+    else if (d4 <= 1024) RN_BWD(4, 2);
+    else RN_BWD(8, 1);
 #undef RN_BWD
     st = check_launch(who);
   } else {
