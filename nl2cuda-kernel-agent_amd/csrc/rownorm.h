@@ -24,7 +24,8 @@
 //    mirrors within each 16-lane row, then v_readlane across the four rows)
 //    plus one LDS step across waves.
 //  * Backward: each of G workgroups holds H = 1 or 2 independent 256-thread
-//    halves; half h of block b walks rows b + h G, every H G-th row after it,
+//    halves (or, for rows longer than 4096 floats, one row group of 512
+//    threads); half h of block b walks rows b + h G, every H G-th row after it,
 //    prefetching the next row's dy and x while it finishes the current one,
 //    and accumulates its partial dw (/ dbias) in registers; the block adds
 //    its halves' partials in LDS and writes one partial row.  The per-block partials ([G][D])
@@ -55,23 +56,30 @@ __device__ __forceinline__ float dot4(f32x4 a, f32x4 b) {
 }
 __device__ __forceinline__ float hsum4(f32x4 a) { return (a[0] + a[1]) + (a[2] + a[3]); }
 
-// Sum over the TPR threads that share a row (TPR = 64 or 256), result in all
-// of them.  `red` is LDS scratch of at least 2 * 4 floats per row group; with
-// TPR = 256 every thread of the block must take part (it holds barriers).
+// Sum over the TPR threads that share a row (TPR = 64, 256 or 512), result
+// in all of them.  `red` is LDS scratch of at least 2 * TPR / 64 floats per
+// row group; with TPR > 64 every thread of the block must take part (it
+// holds barriers).  The wave totals are added in a fixed order.
 template <int TPR>
 __device__ __forceinline__ void row_sum2(float& a, float& b, float* red) {
+  static_assert(TPR == 64 || TPR == 256 || TPR == 512, "row width");
   a = wave_sum_dpp(a);
   b = wave_sum_dpp(b);
-  if (TPR == 256) {
-    const int wave = (threadIdx.x >> 6) & 3;  // the wave within the row's 256 threads
+  if constexpr (TPR > 64) {
+    constexpr int W = TPR / 64;
+    const int wave = (threadIdx.x >> 6) & (W - 1);  // the wave within the row's threads
     __syncthreads();  // red may still be read from the previous use
     if ((threadIdx.x & 63) == 0) {
       red[wave] = a;
-      red[4 + wave] = b;
+      red[W + wave] = b;
     }
     __syncthreads();
     a = (red[0] + red[1]) + (red[2] + red[3]);
-    b = (red[4] + red[5]) + (red[6] + red[7]);
+    b = (red[W] + red[W + 1]) + (red[W + 2] + red[W + 3]);
+    if constexpr (W == 8) {
+      a += (red[4] + red[5]) + (red[6] + red[7]);
+      b += (red[W + 4] + red[W + 5]) + (red[W + 6] + red[W + 7]);
+    }
   }
 }
 
@@ -229,22 +237,25 @@ __global__ __launch_bounds__(kBlock) void rn_fwd_generic_kernel(
 //    waves per SIMD: whole backward 70.3 against 71.8 us at 8192 x 4096,
 //    42.5 against 45.3 at 8192 x 2048.  At V = 1 the rows are short enough
 //    that eight waves meeting at every row's barrier cost more than the
-//    partial rows save (54.3 against 46.3 us at 16384 x 1024); at V = 8 one
-//    half needs more registers than two waves per SIMD allow.
-template <class P, int V, bool FULL, int H>
-__global__ __launch_bounds__(kBlock * H) void rn_bwd_kernel(
+//    partial rows save (54.3 against 46.3 us at 16384 x 1024).
+//  * Rows longer than 4096 floats take C = 2 column groups: 512 threads per
+//    row with V = 4 float4 each.  With 256 threads a thread holds eight
+//    float4 of each of seven row arrays, which leaves one wave per SIMD.
+template <class P, int V, bool FULL, int H, int C>
+__global__ __launch_bounds__(kBlock * H * C) void rn_bwd_kernel(
     const float* __restrict__ dy, const float* __restrict__ x,
     const float* __restrict__ w, const float* __restrict__ stat0,
     const float* __restrict__ stat1, float* __restrict__ dx,
     float* __restrict__ pw, float* __restrict__ pb, int64_t B, int D) {
-  static_assert(H == 1 || H == 2, "one or two halves");
-  __shared__ float red[8 * H];
+  static_assert((H == 1 || H == 2) && (C == 1 || C == 2) && H * C <= 2, "block shape");
+  constexpr int TPR = kBlock * C;  // threads per row
+  __shared__ float red[8 * H * C];
   constexpr int kParts = P::kBias ? 2 : 1;
-  __shared__ f32x4 s_part[H > 1 ? kParts * kBlock * V : 1];  // half 1's partial rows
+  __shared__ f32x4 s_part[H > 1 ? kParts * TPR * V : 1];  // half 1's partial rows
   // The half is wave uniform: take it from lane 0 so that rows, row
   // pointers and the row predicate stay scalar.
   const int hf = H > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x) / kBlock : 0;
-  const int t = threadIdx.x % kBlock;
+  const int t = threadIdx.x % TPR;
   const int D4 = D >> 2;
   const int64_t G = gridDim.x;  // G <= B: every block's half 0 has a row
   const int64_t S = (int64_t)H * G;
@@ -258,7 +269,7 @@ __global__ __launch_bounds__(kBlock * H) void rn_bwd_kernel(
   f32x4 wv[V], aw[V], ab[V], gcur[V], xcur[V], gnext[V], xnext[V];
 #pragma unroll
   for (int k = 0; k < V; ++k) {
-    const int c = t + k * kBlock;
+    const int c = t + k * TPR;
     const f32x4 wk = w4[FULL ? c : min(c, D4 - 1)];
     wv[k] = (FULL || c < D4) ? wk : zero4();
     aw[k] = zero4();
@@ -273,7 +284,7 @@ __global__ __launch_bounds__(kBlock * H) void rn_bwd_kernel(
     const buffer_rsrc rx = make_rsrc(x + r * D, (uint32_t)D * 4u);
 #pragma unroll
     for (int k = 0; k < V; ++k) {
-      const int c = t + k * kBlock;
+      const int c = t + k * TPR;
       g[k] = FULL ? dyr[c] : buffer_load4(rg, (uint32_t)c * 16u, 0);
       xv[k] = FULL ? xr[c] : buffer_load4(rx, (uint32_t)c * 16u, 0);
     }
@@ -308,11 +319,11 @@ __global__ __launch_bounds__(kBlock * H) void rn_bwd_kernel(
     }
     float mg = 0.f, mgx;
     if constexpr (P::kCentered) {
-      row_sum2<kBlock>(sg, sgx, red + 8 * hf);
+      row_sum2<TPR>(sg, sgx, red + 8 * hf);
       mg = sg * inv_d;
       mgx = sgx * inv_d;
     } else {
-      mgx = row_sum1<kBlock>(sgx, red + 8 * hf);
+      mgx = row_sum1<TPR>(sgx, red + 8 * hf);
     }
     {
       // One unconditional store per float4: the resource spans the row (none
@@ -323,7 +334,7 @@ __global__ __launch_bounds__(kBlock * H) void rn_bwd_kernel(
       const buffer_rsrc rdx = make_rsrc(dx + rr * D, has ? (uint32_t)D * 4u : 0u);
 #pragma unroll
       for (int k2 = 0; k2 < V; ++k2) {
-        const int c = t + k2 * kBlock;
+        const int c = t + k2 * TPR;
         buffer_store4(rdx, rs * (gcur[k2] * wv[k2] - mg - xh[k2] * mgx), (uint32_t)c * 16u, 0);
       }
     }
@@ -337,23 +348,23 @@ __global__ __launch_bounds__(kBlock * H) void rn_bwd_kernel(
     if (hf == 1) {
 #pragma unroll
       for (int k = 0; k < V; ++k) {
-        s_part[t + k * kBlock] = aw[k];
-        if constexpr (P::kBias) s_part[kBlock * V + t + k * kBlock] = ab[k];
+        s_part[t + k * TPR] = aw[k];
+        if constexpr (P::kBias) s_part[TPR * V + t + k * TPR] = ab[k];
       }
     }
     __syncthreads();
     if (hf == 1) return;
 #pragma unroll
     for (int k = 0; k < V; ++k) {
-      aw[k] += s_part[t + k * kBlock];
-      if constexpr (P::kBias) ab[k] += s_part[kBlock * V + t + k * kBlock];
+      aw[k] += s_part[t + k * TPR];
+      if constexpr (P::kBias) ab[k] += s_part[TPR * V + t + k * TPR];
     }
   }
   f32x4* pw4 = reinterpret_cast<f32x4*>(pw + (int64_t)blockIdx.x * D);
   f32x4* pb4 = reinterpret_cast<f32x4*>(pb + (int64_t)blockIdx.x * D);
 #pragma unroll
   for (int k = 0; k < V; ++k) {
-    const int c = t + k * kBlock;
+    const int c = t + k * TPR;
     if (FULL || c < D4) {
       pw4[c] = aw[k];
       if constexpr (P::kBias) pb4[c] = ab[k];
@@ -489,7 +500,8 @@ struct Plan {
   bool cached = false;  // row-cached vector path
   int tpr = 256;        // forward threads per row
   int v = 4;            // float4 per thread
-  int halves = 1;       // 256-thread halves per backward block (cached path)
+  int halves = 1;       // backward: 256-thread halves per block, each on its own rows
+  int cols = 1;         // backward: 256-thread column groups per row (cached path)
   int64_t G = 0;        // partial rows of dw / dbias
   int64_t rpb = 0;      // cached: rows per backward block before halving (sets G); generic: rows per partial group
 };
@@ -519,8 +531,12 @@ inline Plan plan(int64_t B, int64_t D, bool aligned) {
     p.rpb = std::max<int64_t>(1, ceil_div(B, s1));
   }
   p.G = B > 0 ? ceil_div(B, p.rpb) : 0;
-  if (p.cached && D / 4 > 256 && D / 4 <= 1024) {  // two halves per block (V = 2, 4)
-    p.halves = 2;
+  // 512-thread backward blocks (two halves, or two column groups for rows
+  // longer than 4096 floats) fill a CU's two waves per SIMD alone: half as
+  // many blocks, so that all of them are resident at once.
+  if (p.cached && D / 4 > 256) {
+    if (D / 4 <= 1024) p.halves = 2;
+    else p.cols = 2;
     p.G = ceil_div(p.G, 2);
   }
   return p;
@@ -595,22 +611,22 @@ int run_backward(const float* dy, const float* x, const float* w, const float* s
   float* pb = pw + p.G * D;
   int st;
   if (p.cached) {
-#define RN_BWD(V, H)                                                                          \
+#define RN_BWD(V, H, C)                                                                       \
   do {                                                                                        \
-    if (D / 4 == 256 * (V))                                                                   \
-      hipLaunchKernelGGL((rn_bwd_kernel<P, V, true, H>), dim3((unsigned)p.G),                 \
-                         dim3(kBlock * (H)), 0, stream, dy, x, w, stat0, stat1, dx, pw, pb, B, \
-                         (int)D);                                                             \
+    if (D / 4 == 256 * (C) * (V))                                                             \
+      hipLaunchKernelGGL((rn_bwd_kernel<P, V, true, H, C>), dim3((unsigned)p.G),              \
+                         dim3(kBlock * (H) * (C)), 0, stream, dy, x, w, stat0, stat1, dx, pw,  \
+                         pb, B, (int)D);                                                      \
     else                                                                                      \
-      hipLaunchKernelGGL((rn_bwd_kernel<P, V, false, H>), dim3((unsigned)p.G),                \
-                         dim3(kBlock * (H)), 0, stream, dy, x, w, stat0, stat1, dx, pw, pb, B, \
-                         (int)D);                                                             \
+      hipLaunchKernelGGL((rn_bwd_kernel<P, V, false, H, C>), dim3((unsigned)p.G),             \
+                         dim3(kBlock * (H) * (C)), 0, stream, dy, x, w, stat0, stat1, dx, pw,  \
+                         pb, B, (int)D);                                                      \
   } while (0)
     const int64_t d4 = D / 4;
-    if (d4 <= 256) RN_BWD(1, 1);
-    else if (d4 <= 512) RN_BWD(2, 2);
-    else if (d4 <= 1024) RN_BWD(4, 2);
-    else RN_BWD(8, 1);
+    if (d4 <= 256) RN_BWD(1, 1, 1);
+    else if (d4 <= 512) RN_BWD(2, 2, 1);
+    else if (p.halves == 2) RN_BWD(4, 2, 1);
+    else RN_BWD(4, 1, 2);
 #undef RN_BWD
     st = check_launch(who);
   } else {

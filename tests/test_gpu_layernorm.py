@@ -65,7 +65,8 @@ def test_layernorm_baseline_8192x4096(seed):
 @pytest.mark.parametrize("b,d", [(5, 4), (33, 64), (17, 100), (300, 256), (64, 1000),
                                  (4096, 1024), (100, 2048), (7, 8192), (3, 8196), (9, 10000),
                                  (1, 1), (2, 3), (1025, 1537), (4099, 1000), (2050, 4100),
-                                 (4097, 4096), (3, 2048), (513, 1028)])
+                                 (4097, 4096), (3, 2048), (513, 1028), (4097, 8192),
+                                 (1000, 6000), (33, 4100)])
 def test_layernorm_shapes(b, d):
     announce(f"layernorm b={b} d={d}")
     _check(*_inputs(b, d, b + d))
