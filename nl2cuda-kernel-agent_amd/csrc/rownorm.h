@@ -47,7 +47,7 @@ namespace rownorm {
 
 constexpr int kBlock = 256;
 constexpr int kFwdBlocks = 512;       // row-cached forward blocks (each walks every 512 RPB-th row)
-constexpr int kBwdBlocks = 512;       // row-cached backward blocks = partial rows of dw / dbias
+constexpr int kBwdBlocks = 512;       // row-cached backward row groups (256 threads each)
 constexpr int kColsumWaves = 16;      // waves of a column-sum workgroup (64 columns)
 constexpr int kGenericMaxSplit = 512; // partial rows of the generic path
 
