@@ -251,7 +251,7 @@ struct FwdPlan {
 };
 
 inline bool plan_forward(int64_t N, int64_t M, FwdPlan& p) {
-  if (N > kMaxTileDim || M > kMaxTileDim) return false;
+  if (N <= 0 || M <= 0 || N > kMaxTileDim || M > kMaxTileDim) return false;  // callers skip empty
   p.n_jt = (int)ceil_div(M, kTile);
   p.ib = ceil_div(N, kFwdRows) * p.n_jt < 2 * kFwdWorkgroups ? 2 : 4;
   const int64_t n_units64 = ceil_div(N, 64 * p.ib) * p.n_jt;
