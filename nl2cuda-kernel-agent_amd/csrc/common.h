@@ -157,6 +157,15 @@ __device__ __forceinline__ void buffer_store4(buffer_rsrc r, f32x4 v, uint32_t l
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, lane_off, wave_off, 0);
 }
 
+__device__ __forceinline__ float buffer_load1(buffer_rsrc r, uint32_t lane_off, int wave_off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, lane_off, wave_off, 0));
+}
+
+__device__ __forceinline__ void buffer_store1(buffer_rsrc r, float v, uint32_t lane_off,
+                                              int wave_off) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, lane_off, wave_off, 0);
+}
+
 // One 16x16x4 fp32 MFMA: acc[m][n] += sum_k A[m][k] * B[k][n].
 // Lane l supplies A[l%16][l/16] in `a` and B[l/16][l%16] in `b`; the result
 // element [4*(l/16)+r][l%16] lives in register r of lane l.

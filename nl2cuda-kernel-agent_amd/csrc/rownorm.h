@@ -17,20 +17,22 @@
 //
 // Design (HBM bound: read x, write y; read dy and x, write dx):
 //  * Row-cached path (D % 4 == 0, 16-byte aligned, D <= 8192): TPR threads
-//    own a row at a time (TPR = 64: a wave, TPR = 256: a workgroup) and walk
-//    every S-th row with the next one in flight; each thread keeps V float4
-//    of the row in registers, so the row is read from HBM exactly once.  Statistics are exact two-pass sums over the
-//    registers; reductions are wave64 DPP lane moves (quad_perm and row
-//    mirrors within each 16-lane row, then v_readlane across the four rows)
-//    plus one LDS step across waves.
-//  * Backward: each of G workgroups holds H = 1 or 2 independent 256-thread
-//    halves (or, for rows longer than 4096 floats, one row group of 512
-//    threads); half h of block b walks rows b + h G, every H G-th row after it,
-//    prefetching the next row's dy and x while it finishes the current one,
-//    and accumulates its partial dw (/ dbias) in registers; the block adds
-//    its halves' partials in LDS and writes one partial row.  The per-block partials ([G][D])
-//    are summed by rn_colsum_kernel in one stream-ordered pass, every sum
-//    in a fixed order, so dw and dbias are deterministic.
+//    own a row at a time (TPR = 64: a wave, TPR = 256 or 512: a workgroup)
+//    and walk every S-th row with the next one in flight; each thread keeps
+//    V float4 of the row in registers, so the row is read from HBM exactly
+//    once.  Statistics are exact two-pass sums over the registers;
+//    reductions are wave64 DPP lane moves (quad_perm and row mirrors within
+//    each 16-lane row, then v_readlane across the four rows) plus, for
+//    rows wider than a wave, one LDS step across waves.
+//  * Backward: each of G workgroups holds H independent row groups (four
+//    waves for rows of at most 512 floats, one or two 256-thread groups up
+//    to 4096, one 512-thread group above); group h of block b walks rows
+//    b + h G, every H G-th row after it, prefetching the next row's dy and
+//    x while it finishes the current one, and accumulates its partial dw
+//    (/ dbias) in registers; the block adds its groups' partials in LDS and
+//    writes one partial row.  The per-block partials ([G][D]) are summed by
+//    rn_colsum_kernel in one stream-ordered pass, every sum in a fixed
+//    order, so dw and dbias are deterministic.
 //  * Any other shape uses generic kernels that re-read x: one workgroup per
 //    row for y / dx, and rn_bwd_generic_partial_kernel (64 columns x a group
 //    of rows per block) for the partial rows, then the same column sums.
@@ -48,6 +50,11 @@ namespace rownorm {
 constexpr int kBlock = 256;
 constexpr int kFwdBlocks = 512;       // row-cached forward blocks (each walks every 512 RPB-th row)
 constexpr int kBwdBlocks = 512;       // row-cached backward row groups (256 threads each)
+constexpr int kBwdWaveGroups1 = 4096; // row-cached backward wave row groups, rows <= 256 floats
+constexpr int kBwdWaveGroups2 = 2048; // ... rows of 257 to 512 floats
+constexpr int kRow16FwdBlocks1 = 2048; // 16-lane-row forward blocks, rows <= 64 floats
+constexpr int kRow16FwdBlocks2 = 512;  // ... rows of 65 to 128 floats
+constexpr int kRow16BwdBlocks = 512;   // 16-lane-row backward blocks = partial rows
 constexpr int kColsumWaves = 16;      // waves of a column-sum workgroup (64 columns)
 constexpr int kGenericMaxSplit = 512; // partial rows of the generic path
 
@@ -222,39 +229,47 @@ __global__ __launch_bounds__(kBlock) void rn_fwd_generic_kernel(
 }
 
 // ----------------------------------------------------------------- backward
-// Level 1: block b of G is H halves of 256 threads (V float4 per thread);
-// half h walks rows b + h G, b + h G + S, b + h G + 2S, ... (S = H G rows per
-// sweep), one row at a time, and the block writes the sum of its halves'
-// partial dw (/ dbias) rows (half 0 + half 1, in that order) to pw[b]
-// (/ pb[b]).  Both halves take the same number of steps, half 0's row count,
-// so they pass the same barriers; a half whose row lies past the end runs
-// the step on a clamped row and keeps nothing of it.
+// Level 1: block b of G is H row groups of TPR threads (V float4 per
+// thread); group h walks rows b + h G, b + h G + S, b + h G + 2S, ... (S =
+// H G rows per sweep), one row at a time, and the block writes the sum of
+// its groups' partial dw (/ dbias) rows (groups 0, 1, ... added in that
+// order) to pw[b] (/ pb[b]).  All groups take the same number of steps,
+// group 0's row count, so they pass the same barriers; a group whose row
+// lies past the end runs the step on a clamped row and keeps nothing of it.
+// Shapes: TPR = 64 (a wave per row, H = 4) for rows of at most 512 floats,
+// TPR = 256 (H = 1 or 2) up to 4096, TPR = 512 (H = 1) above.
 //  * The strided row order keeps the concurrent reads and writes of all
 //    blocks inside one window of about S consecutive rows of each array;
 //    contiguous blocks of rows per block scattered them G row blocks apart
 //    and streamed about 10 % slower (72.6 against 65.0 us at 8192 x 4096).
-//  * Two halves per block (V = 2 and 4) halve the partial rows for the same
+//  * Two 256-thread halves per block (V = 2 and 4) halve the partial rows for the same
 //    waves per SIMD: whole backward 70.3 against 71.8 us at 8192 x 4096,
 //    42.5 against 45.3 at 8192 x 2048.  At V = 1 the rows are short enough
 //    that eight waves meeting at every row's barrier cost more than the
 //    partial rows save (54.3 against 46.3 us at 16384 x 1024).
-//  * Rows longer than 4096 floats take C = 2 column groups: 512 threads per
-//    row with V = 4 float4 each.  With 256 threads a thread holds eight
-//    float4 of each of seven row arrays, which leaves one wave per SIMD.
-template <class P, int V, bool FULL, int H, int C>
-__global__ __launch_bounds__(kBlock * H * C) void rn_bwd_kernel(
+//  * Rows longer than 4096 floats take 512 threads per row with V = 4
+//    float4 each.  With 256 threads a thread holds eight float4 of each of
+//    seven row arrays, which leaves one wave per SIMD.
+//  * Rows of at most 512 floats take a wave each (reductions inside the
+//    wave, no barrier per row): with 256 threads per row, most of them
+//    idle at D = 256, every row paid two workgroup barriers for 1 KB.
+template <class P, int TPR, int V, bool FULL, int H>
+__global__ __launch_bounds__(TPR * H) void rn_bwd_kernel(
     const float* __restrict__ dy, const float* __restrict__ x,
     const float* __restrict__ w, const float* __restrict__ stat0,
     const float* __restrict__ stat1, float* __restrict__ dx,
     float* __restrict__ pw, float* __restrict__ pb, int64_t B, int D) {
-  static_assert((H == 1 || H == 2) && (C == 1 || C == 2) && H * C <= 2, "block shape");
-  constexpr int TPR = kBlock * C;  // threads per row
-  __shared__ float red[8 * H * C];
+  static_assert((TPR == 64 && H == 4) || (TPR == 256 && (H == 1 || H == 2)) ||
+                    (TPR == 512 && H == 1),
+                "block shape");
+  constexpr int kRed = TPR > 64 ? 2 * (TPR / 64) : 1;  // LDS floats per group's row sums
+  __shared__ float red[kRed * H];
   constexpr int kParts = P::kBias ? 2 : 1;
-  __shared__ f32x4 s_part[H > 1 ? kParts * TPR * V : 1];  // half 1's partial rows
-  // The half is wave uniform: take it from lane 0 so that rows, row
+  constexpr int kPart = kParts * TPR * V;  // f32x4 of one group's partial rows
+  __shared__ f32x4 s_part[H > 1 ? (H - 1) * kPart : 1];  // groups 1 .. H-1
+  // The group is wave uniform: take it from lane 0 so that rows, row
   // pointers and the row predicate stay scalar.
-  const int hf = H > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x) / kBlock : 0;
+  const int hf = H > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x) / TPR : 0;
   const int t = threadIdx.x % TPR;
   const int D4 = D >> 2;
   const int64_t G = gridDim.x;  // G <= B: every block's half 0 has a row
@@ -319,11 +334,11 @@ __global__ __launch_bounds__(kBlock * H * C) void rn_bwd_kernel(
     }
     float mg = 0.f, mgx;
     if constexpr (P::kCentered) {
-      row_sum2<TPR>(sg, sgx, red + 8 * hf);
+      row_sum2<TPR>(sg, sgx, red + kRed * hf);
       mg = sg * inv_d;
       mgx = sgx * inv_d;
     } else {
-      mgx = row_sum1<TPR>(sgx, red + 8 * hf);
+      mgx = row_sum1<TPR>(sgx, red + kRed * hf);
     }
     {
       // One unconditional store per float4: the resource spans the row (none
@@ -345,19 +360,24 @@ __global__ __launch_bounds__(kBlock * H * C) void rn_bwd_kernel(
     }
   }
   if constexpr (H > 1) {
-    if (hf == 1) {
+    if (hf > 0) {
+      f32x4* sp = s_part + (hf - 1) * kPart;
 #pragma unroll
       for (int k = 0; k < V; ++k) {
-        s_part[t + k * TPR] = aw[k];
-        if constexpr (P::kBias) s_part[TPR * V + t + k * TPR] = ab[k];
+        sp[t + k * TPR] = aw[k];
+        if constexpr (P::kBias) sp[TPR * V + t + k * TPR] = ab[k];
       }
     }
     __syncthreads();
-    if (hf == 1) return;
+    if (hf > 0) return;
 #pragma unroll
-    for (int k = 0; k < V; ++k) {
-      aw[k] += s_part[t + k * TPR];
-      if constexpr (P::kBias) ab[k] += s_part[TPR * V + t + k * TPR];
+    for (int j = 0; j < H - 1; ++j) {
+      const f32x4* sp = s_part + j * kPart;
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        aw[k] += sp[t + k * TPR];
+        if constexpr (P::kBias) ab[k] += sp[TPR * V + t + k * TPR];
+      }
     }
   }
   f32x4* pw4 = reinterpret_cast<f32x4*>(pw + (int64_t)blockIdx.x * D);
@@ -366,6 +386,232 @@ __global__ __launch_bounds__(kBlock * H * C) void rn_bwd_kernel(
   for (int k = 0; k < V; ++k) {
     const int c = t + k * TPR;
     if (FULL || c < D4) {
+      pw4[c] = aw[k];
+      if constexpr (P::kBias) pb4[c] = ab[k];
+    }
+  }
+}
+
+// ------------------------------------------- rows of at most 128 floats
+// Sum over each 16-lane row of the wave.  Every lane of the row gets the
+// same bits: each step adds the same two partial sums, in one order or the
+// other.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x141>(v);
+  v += dpp_mov<0x140>(v);
+  return v;
+}
+
+// Rows of at most 128 floats (V = 1 or 2 float4 per lane) take 16 lanes
+// each: four consecutive rows per wave, 16 per block.  Block b walks row
+// sets b, b + G, b + 2G, ... (16 rows each) with the next set's loads in
+// flight.  Loads and stores go through buffer resources over the wave's
+// rows that exist (the first min(4, B - row) of its four), and a lane past
+// its row's end has an offset outside any of them: loads read zeros,
+// stores write nothing, and no memory operation sits under a branch or
+// depends on a per-step select (the compiler turns such a select into a
+// branch).  With a wave per row, 48 of 64 lanes idled at D = 64.
+constexpr uint32_t kOutside = 0x7FFFFFF0u;  // past any resource used here; no 32-bit wrap
+
+template <class P, int V>
+__global__ __launch_bounds__(kBlock) void rn_fwd_row16_kernel(
+    const float* __restrict__ x, const float* __restrict__ w,
+    const float* __restrict__ bias, float* __restrict__ y,
+    float* __restrict__ stat0, float* __restrict__ stat1, int64_t B,
+    int D, float eps) {
+  constexpr int RPB = kBlock / 16;
+  const int lane = threadIdx.x & 63;
+  const int j = lane >> 4;  // the lane's row among the wave's four
+  const int t = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x) >> 6;
+  const int D4 = D >> 2;
+  const int64_t S = (int64_t)gridDim.x * RPB;
+  const int64_t rw0 = (int64_t)blockIdx.x * RPB + 4 * wave;  // the wave's first row
+  if (rw0 >= B) return;  // wave uniform; no barriers below
+  const int64_t rwl = rw0 + (B - 1 - rw0) / S * S;       // its last row set
+  const uint32_t rbytes = (uint32_t)D * 4u;
+  auto rows = [&](int64_t rw) { return (uint32_t)min(B - rw, (int64_t)4); };
+  const f32x4* w4 = reinterpret_cast<const f32x4*>(w);
+  const f32x4* b4 = reinterpret_cast<const f32x4*>(bias);
+  uint32_t off[V];
+  f32x4 wv[V], bv[V];
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    const int c = t + 16 * k;
+    off[k] = c < D4 ? (uint32_t)j * rbytes + (uint32_t)c * 16u : kOutside;
+    wv[k] = w4[min(c, D4 - 1)];
+    if constexpr (P::kBias) bv[k] = b4[min(c, D4 - 1)];
+  }
+  const uint32_t soff = t == 0 ? (uint32_t)j * 4u : kOutside;
+  auto load = [&](int64_t rw, f32x4 (&v)[V]) {
+    const buffer_rsrc r = make_rsrc(x + rw * D, rows(rw) * rbytes);
+#pragma unroll
+    for (int k = 0; k < V; ++k) v[k] = buffer_load4(r, off[k], 0);
+  };
+  f32x4 cur[V], nxt[V];
+  load(rw0, cur);
+  const float inv_d = 1.f / (float)D;
+  for (int64_t rw = rw0; rw < B; rw += S) {
+    load(min(rw + S, rwl), nxt);  // the last set re-reads itself
+    // keep the next set's loads ahead of all work on this one
+    __builtin_amdgcn_sched_barrier(0);
+    float mu = 0.f;
+    if constexpr (P::kCentered) {
+      float sx = 0.f;
+#pragma unroll
+      for (int k = 0; k < V; ++k) sx += hsum4(cur[k]);  // zeros past the row
+      mu = row16_sum(sx) * inv_d;
+    }
+    float q = 0.f;
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      const f32x4 dv = cur[k] - mu;
+      q += t + 16 * k < D4 ? dot4(dv, dv) : 0.f;
+    }
+    const float ss = row16_sum(q) * (P::kCentered ? inv_d : 1.f) + eps;
+    const float rs = 1.f / sqrtf(ss);
+    const uint32_t n = rows(rw);
+    if constexpr (P::kCentered) buffer_store1(make_rsrc(stat0 + rw, 4u * n), mu, soff, 0);
+    buffer_store1(make_rsrc(stat1 + rw, 4u * n), P::stat1(rs, ss), soff, 0);
+    const buffer_rsrc ry = make_rsrc(y + rw * D, n * rbytes);
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      f32x4 yv = (cur[k] - mu) * rs * wv[k];
+      if constexpr (P::kBias) yv += bv[k];
+      buffer_store4(ry, yv, off[k], 0);
+    }
+#pragma unroll
+    for (int k = 0; k < V; ++k) cur[k] = nxt[k];
+  }
+}
+
+// Backward for the same rows: the layout of rn_fwd_row16_kernel, with the
+// row statistics loaded beside the row data (a row set ahead); partial dw
+// (/ dbias) in registers per lane.  At the end the four row groups of a
+// wave are added by two lane exchanges (16 apart, then 32 apart) and the
+// four waves in LDS (0 + 1 + 2 + 3), and the block writes one partial row.
+template <class P, int V>
+__global__ __launch_bounds__(kBlock) void rn_bwd_row16_kernel(
+    const float* __restrict__ dy, const float* __restrict__ x,
+    const float* __restrict__ w, const float* __restrict__ stat0,
+    const float* __restrict__ stat1, float* __restrict__ dx,
+    float* __restrict__ pw, float* __restrict__ pb, int64_t B, int D) {
+  constexpr int RPB = kBlock / 16;
+  constexpr int kParts = P::kBias ? 2 : 1;
+  constexpr int kPart = kParts * 16 * V;  // f32x4 of one wave's partial rows
+  __shared__ f32x4 s_part[3 * kPart];     // waves 1 .. 3
+  const int lane = threadIdx.x & 63;
+  const int j = lane >> 4;
+  const int t = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x) >> 6;
+  const int D4 = D >> 2;
+  const int64_t S = (int64_t)gridDim.x * RPB;
+  const int64_t rw0 = (int64_t)blockIdx.x * RPB + 4 * wave;
+  const uint32_t rbytes = (uint32_t)D * 4u;
+  auto rows = [&](int64_t rw) { return (uint32_t)min(B - rw, (int64_t)4); };
+  const f32x4* w4 = reinterpret_cast<const f32x4*>(w);
+  uint32_t off[V];
+  f32x4 wv[V], aw[V], ab[V];
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    const int c = t + 16 * k;
+    off[k] = c < D4 ? (uint32_t)j * rbytes + (uint32_t)c * 16u : kOutside;
+    const f32x4 wk = w4[min(c, D4 - 1)];
+    wv[k] = c < D4 ? wk : zero4();
+    aw[k] = zero4();
+    ab[k] = zero4();
+  }
+  const uint32_t soff = (uint32_t)j * 4u;
+  if (rw0 < B) {  // wave uniform: a wave past the end only adds zeros below
+    const int64_t rwl = rw0 + (B - 1 - rw0) / S * S;
+    struct Set {
+      f32x4 g[V], xv[V];
+      float s0, s1;
+    };
+    auto load = [&](int64_t rw, Set& q) {
+      const uint32_t n = rows(rw);
+      const buffer_rsrc rg = make_rsrc(dy + rw * D, n * rbytes);
+      const buffer_rsrc rx = make_rsrc(x + rw * D, n * rbytes);
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        q.g[k] = buffer_load4(rg, off[k], 0);
+        q.xv[k] = buffer_load4(rx, off[k], 0);
+      }
+      q.s0 = P::kCentered ? buffer_load1(make_rsrc(stat0 + rw, 4u * n), soff, 0) : 0.f;
+      q.s1 = buffer_load1(make_rsrc(stat1 + rw, 4u * n), soff, 0);
+    };
+    Set cur, nxt;
+    load(rw0, cur);
+    const float inv_d = 1.f / (float)D;
+    for (int64_t rw = rw0; rw < B; rw += S) {
+      load(min(rw + S, rwl), nxt);
+      __builtin_amdgcn_sched_barrier(0);  // the next set's loads ahead of this set's work
+      const bool ok = (uint32_t)j < rows(rw);
+      const float mu = cur.s0;
+      const float rs = P::rs(cur.s1);
+      float sg = 0.f, sgx = 0.f;
+      f32x4 xh[V];
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        xh[k] = (cur.xv[k] - mu) * rs;
+        const f32x4 g = cur.g[k] * wv[k];
+        if constexpr (P::kCentered) sg += hsum4(g);
+        sgx += dot4(g, xh[k]);
+      }
+      const float mg = P::kCentered ? row16_sum(sg) * inv_d : 0.f;
+      const float mgx = row16_sum(sgx) * (P::kCentered ? inv_d : 1.f);
+      const buffer_rsrc rdx = make_rsrc(dx + rw * D, rows(rw) * rbytes);
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        buffer_store4(rdx, rs * (cur.g[k] * wv[k] - mg - xh[k] * mgx), off[k], 0);
+        // a row past B has no statistics (zeros, possibly an infinite rs):
+        // select, so that nothing of it reaches the partial sums
+        aw[k] = ok ? aw[k] + cur.g[k] * xh[k] : aw[k];
+        if constexpr (P::kBias) ab[k] = ok ? ab[k] + cur.g[k] : ab[k];
+      }
+      cur = nxt;
+    }
+  }
+  // The wave's four row groups hold the same columns: add them across lanes.
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      aw[k][e] += __shfl_xor(aw[k][e], 16, 64);
+      aw[k][e] += __shfl_xor(aw[k][e], 32, 64);
+      if constexpr (P::kBias) {
+        ab[k][e] += __shfl_xor(ab[k][e], 16, 64);
+        ab[k][e] += __shfl_xor(ab[k][e], 32, 64);
+      }
+    }
+  }
+  if (wave > 0 && j == 0) {
+    f32x4* sp = s_part + (wave - 1) * kPart;
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      sp[t + 16 * k] = aw[k];
+      if constexpr (P::kBias) sp[16 * V + t + 16 * k] = ab[k];
+    }
+  }
+  __syncthreads();
+  if (wave > 0 || j > 0) return;
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    const f32x4* sp = s_part + q * kPart;
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      aw[k] += sp[t + 16 * k];
+      if constexpr (P::kBias) ab[k] += sp[16 * V + t + 16 * k];
+    }
+  }
+  f32x4* pw4 = reinterpret_cast<f32x4*>(pw + (int64_t)blockIdx.x * D);
+  f32x4* pb4 = reinterpret_cast<f32x4*>(pb + (int64_t)blockIdx.x * D);
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    const int c = t + 16 * k;
+    if (c < D4) {
       pw4[c] = aw[k];
       if constexpr (P::kBias) pb4[c] = ab[k];
     }
@@ -500,44 +746,70 @@ struct Plan {
   bool cached = false;  // row-cached vector path
   int tpr = 256;        // forward threads per row
   int v = 4;            // float4 per thread
-  int halves = 1;       // backward: 256-thread halves per block, each on its own rows
-  int cols = 1;         // backward: 256-thread column groups per row (cached path)
+  int btpr = 256;       // backward (cached): threads per row
+  int bv = 1;           // backward (cached): float4 per thread
+  int bh = 1;           // backward (cached): row groups per block
   int64_t G = 0;        // partial rows of dw / dbias
-  int64_t rpb = 0;      // cached: rows per backward block before halving (sets G); generic: rows per partial group
+  int64_t rpb = 0;      // generic path: rows per partial group
 };
+
+// Row groups of at most `target` with ceil(B / target) rows each.
+inline int64_t row_groups(int64_t B, int64_t target) {
+  return ceil_div(B, std::max<int64_t>(1, ceil_div(B, target)));
+}
 
 inline Plan plan(int64_t B, int64_t D, bool aligned) {
   Plan p;
   p.cached = aligned && D % 4 == 0 && D <= 8192;
-  if (p.cached) {
-    const int64_t d4 = D / 4;
-    if (d4 <= 64) {
-      p.tpr = 64;
-      p.v = 1;
-    } else if (d4 <= 256) {
-      p.tpr = 64;
-      p.v = 4;
-    } else {
-      p.tpr = 256;
-      p.v = d4 <= 512 ? 2 : d4 <= 1024 ? 4 : 8;
-    }
-    p.rpb = std::max<int64_t>(1, ceil_div(B, kBwdBlocks));
-  } else {
+  if (!p.cached) {
     // ~2048 blocks of 64 columns x (B / S1) rows
     const int64_t slices = ceil_div(D, 64);
     const int64_t s1 = std::min<int64_t>(
         std::min<int64_t>(std::max<int64_t>(1, ceil_div(2048, slices)), kGenericMaxSplit),
         std::max<int64_t>(B, 1));
     p.rpb = std::max<int64_t>(1, ceil_div(B, s1));
+    p.G = B > 0 ? ceil_div(B, p.rpb) : 0;
+    return p;
   }
-  p.G = B > 0 ? ceil_div(B, p.rpb) : 0;
-  // 512-thread backward blocks (two halves, or two column groups for rows
-  // longer than 4096 floats) fill a CU's two waves per SIMD alone: half as
-  // many blocks, so that all of them are resident at once.
-  if (p.cached && D / 4 > 256) {
-    if (D / 4 <= 1024) p.halves = 2;
-    else p.cols = 2;
-    p.G = ceil_div(p.G, 2);
+  const int64_t d4 = D / 4;
+  if (d4 <= 32) {  // 16 lanes per row, both directions
+    p.tpr = p.btpr = 16;
+    p.v = p.bv = d4 <= 16 ? 1 : 2;
+    p.bh = 16;
+    p.G = B > 0 ? std::min<int64_t>(ceil_div(B, 16), kRow16BwdBlocks) : 0;
+    return p;
+  }
+  if (d4 <= 64) {
+    p.tpr = 64;
+    p.v = 1;
+  } else if (d4 <= 256) {
+    p.tpr = 64;
+    p.v = 4;
+  } else {
+    p.tpr = 256;
+    p.v = d4 <= 512 ? 2 : d4 <= 1024 ? 4 : 8;
+  }
+  if (B == 0) return p;
+  if (d4 <= 128) {  // a wave per row, four per block
+    p.btpr = 64;
+    p.bv = d4 <= 64 ? 1 : 2;
+    p.bh = 4;
+    p.G = ceil_div(row_groups(B, p.bv == 1 ? kBwdWaveGroups1 : kBwdWaveGroups2), 4);
+  } else if (d4 <= 256) {
+    p.bv = 1;
+    p.G = row_groups(B, kBwdBlocks);
+  } else {
+    // 512-thread blocks (two halves, or 512 threads per row above 4096
+    // floats) fill a CU's two waves per SIMD alone: half as many blocks,
+    // so that all of them are resident at once.
+    if (d4 <= 1024) {
+      p.bv = d4 <= 512 ? 2 : 4;
+      p.bh = 2;
+    } else {
+      p.btpr = 512;
+      p.bv = 4;
+    }
+    p.G = ceil_div(row_groups(B, kBwdBlocks), 2);
   }
   return p;
 }
@@ -566,6 +838,17 @@ int run_forward(const float* x, const float* w, const float* bias, float* y, flo
   const bool aligned = aligned16(x) && aligned16(w) && (!P::kBias || aligned16(bias)) &&
                        aligned16(y);
   const Plan p = plan(B, D, aligned);
+  if (p.cached && p.tpr == 16) {
+    const dim3 grid((unsigned)std::min<int64_t>(
+        ceil_div(B, 16), p.v == 1 ? kRow16FwdBlocks1 : kRow16FwdBlocks2));
+    if (p.v == 1)
+      hipLaunchKernelGGL((rn_fwd_row16_kernel<P, 1>), grid, dim3(kBlock), 0, stream, x, w, bias,
+                         y, stat0, stat1, B, (int)D, eps);
+    else
+      hipLaunchKernelGGL((rn_fwd_row16_kernel<P, 2>), grid, dim3(kBlock), 0, stream, x, w, bias,
+                         y, stat0, stat1, B, (int)D, eps);
+    return check_launch(who);
+  }
   if (p.cached) {
     const int rpb = kBlock / p.tpr;
     const dim3 grid((unsigned)std::min<int64_t>(ceil_div(B, rpb), kFwdBlocks));
@@ -611,22 +894,29 @@ int run_backward(const float* dy, const float* x, const float* w, const float* s
   float* pb = pw + p.G * D;
   int st;
   if (p.cached) {
-#define RN_BWD(V, H, C)                                                                       \
+#define RN_BWD(TPR, V, H)                                                                     \
   do {                                                                                        \
-    if (D / 4 == 256 * (C) * (V))                                                             \
-      hipLaunchKernelGGL((rn_bwd_kernel<P, V, true, H, C>), dim3((unsigned)p.G),              \
-                         dim3(kBlock * (H) * (C)), 0, stream, dy, x, w, stat0, stat1, dx, pw,  \
-                         pb, B, (int)D);                                                      \
+    if (D / 4 == (TPR) * (V))                                                                 \
+      hipLaunchKernelGGL((rn_bwd_kernel<P, TPR, V, true, H>), dim3((unsigned)p.G),            \
+                         dim3((TPR) * (H)), 0, stream, dy, x, w, stat0, stat1, dx, pw, pb, B, \
+                         (int)D);                                                             \
     else                                                                                      \
-      hipLaunchKernelGGL((rn_bwd_kernel<P, V, false, H, C>), dim3((unsigned)p.G),             \
-                         dim3(kBlock * (H) * (C)), 0, stream, dy, x, w, stat0, stat1, dx, pw,  \
-                         pb, B, (int)D);                                                      \
+      hipLaunchKernelGGL((rn_bwd_kernel<P, TPR, V, false, H>), dim3((unsigned)p.G),           \
+                         dim3((TPR) * (H)), 0, stream, dy, x, w, stat0, stat1, dx, pw, pb, B, \
+                         (int)D);                                                             \
   } while (0)
-    const int64_t d4 = D / 4;
-    if (d4 <= 256) RN_BWD(1, 1, 1);
-    else if (d4 <= 512) RN_BWD(2, 2, 1);
-    else if (p.halves == 2) RN_BWD(4, 2, 1);
-    else RN_BWD(4, 1, 2);
+    if (p.btpr == 16 && p.bv == 1)
+      hipLaunchKernelGGL((rn_bwd_row16_kernel<P, 1>), dim3((unsigned)p.G), dim3(kBlock), 0,
+                         stream, dy, x, w, stat0, stat1, dx, pw, pb, B, (int)D);
+    else if (p.btpr == 16)
+      hipLaunchKernelGGL((rn_bwd_row16_kernel<P, 2>), dim3((unsigned)p.G), dim3(kBlock), 0,
+                         stream, dy, x, w, stat0, stat1, dx, pw, pb, B, (int)D);
+    else if (p.btpr == 64 && p.bv == 1) RN_BWD(64, 1, 4);
+    else if (p.btpr == 64) RN_BWD(64, 2, 4);
+    else if (p.btpr == 256 && p.bv == 1) RN_BWD(256, 1, 1);
+    else if (p.bv == 2) RN_BWD(256, 2, 2);
+    else if (p.btpr == 256) RN_BWD(256, 4, 2);
+    else RN_BWD(512, 4, 1);
 #undef RN_BWD
     st = check_launch(who);
   } else {

@@ -62,7 +62,9 @@ def test_l2norm_bench_shapes(n, d, seed):
 @pytest.mark.parametrize("n,d", [(5, 4), (33, 64), (17, 100), (300, 256), (64, 1000),
                                  (40, 1024), (9, 2048), (3, 8192), (2, 8196), (7, 12000),
                                  (1, 1), (4099, 1000), (2050, 4100), (4097, 4096),
-                                 (3, 2048), (513, 1028), (4097, 8192), (1000, 6000)])
+                                 (3, 2048), (513, 1028), (4097, 8192), (1000, 6000),
+                                 (4099, 512), (2050, 300),
+                                 (16385, 64), (1000, 128), (4097, 96)])
 def test_l2norm_shapes(n, d):
     announce(f"l2norm_scale [{n}, {d}]")
     _check(*_inputs(n, d, n + d))

@@ -66,7 +66,9 @@ def test_layernorm_baseline_8192x4096(seed):
                                  (4096, 1024), (100, 2048), (7, 8192), (3, 8196), (9, 10000),
                                  (1, 1), (2, 3), (1025, 1537), (4099, 1000), (2050, 4100),
                                  (4097, 4096), (3, 2048), (513, 1028), (4097, 8192),
-                                 (1000, 6000), (33, 4100)])
+                                 (1000, 6000), (33, 4100),
+                                 (4099, 512), (2050, 300), (16384, 256),
+                                 (16385, 64), (1000, 128), (4097, 96), (3, 128), (70, 8)])
 def test_layernorm_shapes(b, d):
     announce(f"layernorm b={b} d={d}")
     _check(*_inputs(b, d, b + d))
@@ -102,7 +104,7 @@ def test_layernorm_constant_rows():
     _check(x, w, b, dy)
 
 
-@pytest.mark.parametrize("b,d", [(64, 4096), (96, 1024)])
+@pytest.mark.parametrize("b,d", [(64, 4096), (96, 1024), (70, 64)])
 def test_layernorm_nan_row_stays_in_its_row(b, d):
     """A NaN in one row of x makes that row of y and dx NaN (its mean and
     variance are NaN, as in torch's layer_norm) and, through the column sums,
