@@ -17,22 +17,23 @@
 //
 // Design (HBM bound: read x, write y; read dy and x, write dx):
 //  * Row-cached path (D % 4 == 0, 16-byte aligned, D <= 8192): TPR threads
-//    own a row at a time (TPR = 64: a wave, TPR = 256 or 512: a workgroup)
-//    and walk every S-th row with the next one in flight; each thread keeps
-//    V float4 of the row in registers, so the row is read from HBM exactly
-//    once.  Statistics are exact two-pass sums over the registers;
-//    reductions are wave64 DPP lane moves (quad_perm and row mirrors within
-//    each 16-lane row, then v_readlane across the four rows) plus, for
-//    rows wider than a wave, one LDS step across waves.
-//  * Backward: each of G workgroups holds H independent row groups (four
-//    waves for rows of at most 512 floats, one or two 256-thread groups up
-//    to 4096, one 512-thread group above); group h of block b walks rows
-//    b + h G, every H G-th row after it, prefetching the next row's dy and
-//    x while it finishes the current one, and accumulates its partial dw
-//    (/ dbias) in registers; the block adds its groups' partials in LDS and
-//    writes one partial row.  The per-block partials ([G][D]) are summed by
-//    rn_colsum_kernel in one stream-ordered pass, every sum in a fixed
-//    order, so dw and dbias are deterministic.
+//    own a row at a time (16 lanes for rows of at most 128 floats, a wave,
+//    or a workgroup of 256 or 512 threads for long rows) and walk every
+//    S-th row with the next one in flight; each thread keeps V float4 of
+//    the row in registers, so the row is read from HBM exactly once.
+//    Statistics are exact two-pass sums over the registers; reductions are
+//    wave64 DPP lane moves (quad_perm and row mirrors within each 16-lane
+//    row, then v_readlane across the four rows) plus, for rows wider than a
+//    wave, one LDS step across waves.
+//  * Backward: each of G workgroups holds H independent row groups (16
+//    rows of 16 lanes up to 128 floats, four waves up to 1024, two
+//    256-thread groups up to 4096, one 512-thread group above) that walk
+//    their rows G row groups apart, prefetching the next row's dy and x
+//    while they finish the current one, and accumulate partial dw
+//    (/ dbias) in registers; the block adds its groups' partials (in a
+//    fixed order) and writes one partial row.  The per-block partials
+//    ([G][D]) are summed by rn_colsum_kernel in one stream-ordered pass,
+//    every sum in a fixed order, so dw and dbias are deterministic.
 //  * Any other shape uses generic kernels that re-read x: one workgroup per
 //    row for y / dx, and rn_bwd_generic_partial_kernel (64 columns x a group
 //    of rows per block) for the partial rows, then the same column sums.
@@ -51,7 +52,7 @@ constexpr int kBlock = 256;
 constexpr int kFwdBlocks = 512;       // row-cached forward blocks (each walks every 512 RPB-th row)
 constexpr int kBwdBlocks = 512;       // row-cached backward row groups (256 threads each)
 constexpr int kBwdWaveGroups1 = 4096; // row-cached backward wave row groups, rows <= 256 floats
-constexpr int kBwdWaveGroups2 = 2048; // ... rows of 257 to 512 floats
+constexpr int kBwdWaveGroups2 = 2048; // ... rows of 257 to 1024 floats
 constexpr int kRow16FwdBlocks1 = 2048; // 16-lane-row forward blocks, rows <= 64 floats
 constexpr int kRow16FwdBlocks2 = 512;  // ... rows of 65 to 128 floats
 constexpr int kRow16BwdBlocks = 512;   // 16-lane-row backward blocks = partial rows
@@ -236,21 +237,20 @@ __global__ __launch_bounds__(kBlock) void rn_fwd_generic_kernel(
 // order) to pw[b] (/ pb[b]).  All groups take the same number of steps,
 // group 0's row count, so they pass the same barriers; a group whose row
 // lies past the end runs the step on a clamped row and keeps nothing of it.
-// Shapes: TPR = 64 (a wave per row, H = 4) for rows of at most 512 floats,
-// TPR = 256 (H = 1 or 2) up to 4096, TPR = 512 (H = 1) above.
+// Shapes: TPR = 64 (a wave per row, H = 4) for rows of 129 to 1024 floats,
+// TPR = 256 (H = 2) up to 4096, TPR = 512 (H = 1) above; shorter rows take
+// rn_bwd_row16_kernel.
 //  * The strided row order keeps the concurrent reads and writes of all
 //    blocks inside one window of about S consecutive rows of each array;
 //    contiguous blocks of rows per block scattered them G row blocks apart
 //    and streamed about 10 % slower (72.6 against 65.0 us at 8192 x 4096).
 //  * Two 256-thread halves per block (V = 2 and 4) halve the partial rows for the same
 //    waves per SIMD: whole backward 70.3 against 71.8 us at 8192 x 4096,
-//    42.5 against 45.3 at 8192 x 2048.  At V = 1 the rows are short enough
-//    that eight waves meeting at every row's barrier cost more than the
-//    partial rows save (54.3 against 46.3 us at 16384 x 1024).
+//    42.5 against 45.3 at 8192 x 2048.
 //  * Rows longer than 4096 floats take 512 threads per row with V = 4
 //    float4 each.  With 256 threads a thread holds eight float4 of each of
 //    seven row arrays, which leaves one wave per SIMD.
-//  * Rows of at most 512 floats take a wave each (reductions inside the
+//  * Rows of at most 1024 floats take a wave each (reductions inside the
 //    wave, no barrier per row): with 256 threads per row, most of them
 //    idle at D = 256, every row paid two workgroup barriers for 1 KB.
 template <class P, int TPR, int V, bool FULL, int H>
@@ -790,14 +790,11 @@ inline Plan plan(int64_t B, int64_t D, bool aligned) {
     p.v = d4 <= 512 ? 2 : d4 <= 1024 ? 4 : 8;
   }
   if (B == 0) return p;
-  if (d4 <= 128) {  // a wave per row, four per block
+  if (d4 <= 256) {  // a wave per row, four per block
     p.btpr = 64;
-    p.bv = d4 <= 64 ? 1 : 2;
+    p.bv = d4 <= 64 ? 1 : d4 <= 128 ? 2 : d4 <= 192 ? 3 : 4;
     p.bh = 4;
     p.G = ceil_div(row_groups(B, p.bv == 1 ? kBwdWaveGroups1 : kBwdWaveGroups2), 4);
-  } else if (d4 <= 256) {
-    p.bv = 1;
-    p.G = row_groups(B, kBwdBlocks);
   } else {
     // 512-thread blocks (two halves, or 512 threads per row above 4096
     // floats) fill a CU's two waves per SIMD alone: half as many blocks,
@@ -912,8 +909,9 @@ int run_backward(const float* dy, const float* x, const float* w, const float* s
       hipLaunchKernelGGL((rn_bwd_row16_kernel<P, 2>), dim3((unsigned)p.G), dim3(kBlock), 0,
                          stream, dy, x, w, stat0, stat1, dx, pw, pb, B, (int)D);
     else if (p.btpr == 64 && p.bv == 1) RN_BWD(64, 1, 4);
-    else if (p.btpr == 64) RN_BWD(64, 2, 4);
-    else if (p.btpr == 256 && p.bv == 1) RN_BWD(256, 1, 1);
+    else if (p.btpr == 64 && p.bv == 2) RN_BWD(64, 2, 4);
+    else if (p.btpr == 64 && p.bv == 3) RN_BWD(64, 3, 4);
+    else if (p.btpr == 64) RN_BWD(64, 4, 4);
     else if (p.bv == 2) RN_BWD(256, 2, 2);
     else if (p.btpr == 256) RN_BWD(256, 4, 2);
     else RN_BWD(512, 4, 1);

@@ -68,7 +68,8 @@ def test_layernorm_baseline_8192x4096(seed):
                                  (4097, 4096), (3, 2048), (513, 1028), (4097, 8192),
                                  (1000, 6000), (33, 4100),
                                  (4099, 512), (2050, 300), (16384, 256),
-                                 (16385, 64), (1000, 128), (4097, 96), (3, 128), (70, 8)])
+                                 (16385, 64), (1000, 128), (4097, 96), (3, 128), (70, 8),
+                                 (4099, 600), (1030, 768), (257, 1020)])
 def test_layernorm_shapes(b, d):
     announce(f"layernorm b={b} d={d}")
     _check(*_inputs(b, d, b + d))
