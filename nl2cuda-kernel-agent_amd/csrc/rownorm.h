@@ -784,7 +784,7 @@ inline Plan plan(int64_t B, int64_t D, bool aligned) {
     p.v = 1;
   } else if (d4 <= 256) {
     p.tpr = 64;
-    p.v = 4;
+    p.v = (int)ceil_div(d4, 64);  // 2, 3 or 4
   } else {
     p.tpr = 256;
     p.v = d4 <= 512 ? 2 : d4 <= 1024 ? 4 : 8;
@@ -859,6 +859,8 @@ int run_forward(const float* x, const float* w, const float* bias, float* y, flo
                          w, bias, y, stat0, stat1, B, (int)D, eps);                          \
   } while (0)
     if (p.tpr == 64 && p.v == 1) RN_FWD(64, 1);
+    else if (p.tpr == 64 && p.v == 2) RN_FWD(64, 2);
+    else if (p.tpr == 64 && p.v == 3) RN_FWD(64, 3);
     else if (p.tpr == 64) RN_FWD(64, 4);
     else if (p.v == 2) RN_FWD(256, 2);
     else if (p.v == 4) RN_FWD(256, 4);
