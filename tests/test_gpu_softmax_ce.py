@@ -81,10 +81,13 @@ def test_softmax_ce_bench_shapes(b, c, seed):
 
 # width classes of the row-cached forward: C/4 <= 64, <= 256 (one wave per
 # row), <= 512, <= 1024, <= 2048 (a workgroup per row), each full and ragged;
-# then the generic kernel (C % 4 != 0, C > 8192)
+# then the one-pass workgroup-per-row kernel (C % 4 != 0, C > 8192; float4
+# or scalar loads) and the lane-per-row kernel (C <= 8, 16, 32)
 @pytest.mark.parametrize("b,c", [(37, 4), (100, 100), (64, 256), (70, 1000), (5, 1024),
                                  (33, 1500), (16, 2048), (9, 3000), (12, 4096), (7, 6000),
-                                 (3, 8192), (1, 1), (20, 7), (6, 8196), (4, 12000)])
+                                 (3, 8192), (1, 1), (20, 7), (6, 8196), (4, 12000),
+                                 (1000, 32000), (33, 50257), (5, 128256), (4000, 10), (70, 32),
+                                 (300, 17), (64, 33), (1025, 8), (2, 2)])
 def test_softmax_ce_shapes(b, c):
     announce(f"softmax_ce [{b}, {c}]")
     _check(*_inputs(b, c, b + c))
