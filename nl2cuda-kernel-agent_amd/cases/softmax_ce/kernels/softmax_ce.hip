@@ -11,7 +11,8 @@
 // softmax_ce_forward.cu:14-50, softmax_ce_backward.cu:13-56).
 //
 // Design (HBM bound):
-//  * Forward: TPR threads own a row (TPR = 64 up to C = 1024, else 256) and
+//  * Forward: TPR threads own a row (TPR = 16 up to C = 128, 64 up to
+//    C = 1024, else 256) and
 //    keep its V float4 in registers, so the row is read once; every thread
 //    issues the loads of R rows before using any.  The row max, then sum
 //    exp2((x - max) log2 e), reduced with DPP lane moves (plus one LDS step
@@ -31,8 +32,8 @@
 //    and label are read once; shorter rows use a flat grid-stride kernel.
 //  * A label outside [0, C) makes its row's loss term and gradient NaN (the
 //    reference would index out of the row; torch raises).
-//  * Rows of at most 32 classes (any alignment) take a lane each in the
-//    forward.  C not a multiple of 4, misaligned rows or C > 8192 take a
+//  * Unaligned rows (or C % 4 != 0) of at most 32 classes take a lane each
+//    in the forward.  C not a multiple of 4, misaligned rows or C > 8192 take a
 //    workgroup per row in the forward (one pass with a running maximum,
 //    float4 loads when aligned) and the flat backward.
 #include <algorithm>
@@ -60,11 +61,17 @@ constexpr size_t kWorkspaceBytes = kStatusOffset + 8;
 constexpr unsigned kSpinLimit = 1u << 24;  // hang guard for workgroup 0's wait
 
 
-// Reduce N values per thread over the TPR threads that share a row (TPR = 64:
-// one wave; TPR = 256: the workgroup, through `red`, >= 4 * N floats); the
-// results land in every thread.  MAX selects fmaxf, else +.
+// Reduce N values per thread over the TPR threads that share a row (TPR = 16:
+// a 16-lane row of the wave; 64: one wave; 256: the workgroup, through
+// `red`, >= 4 * N floats); the results land in every thread.  MAX selects
+// fmaxf, else +.
 template <int TPR, int N, bool MAX>
 __device__ __forceinline__ void row_reduce(float (&a)[N], float* red) {
+  if constexpr (TPR == 16) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) a[j] = MAX ? nl2k::row16_max_dpp(a[j]) : nl2k::row16_sum_dpp(a[j]);
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < N; ++j) a[j] = MAX ? nl2k::wave_max_dpp(a[j]) : nl2k::wave_sum_dpp(a[j]);
   if (TPR == 256) {
@@ -304,7 +311,7 @@ __global__ __launch_bounds__(kBlock) void sce_fwd_long_kernel(
   if (blockIdx.x == 0) sum_partials(slots, key, (int)gridDim.x, B, loss, red);
 }
 
-// Forward for rows of at most CM <= 32 classes, any alignment: a lane per
+// Forward for rows of at most CM <= 32 classes that are not float4 rows: a lane per
 // row with its logits in registers (a wave's loads cover 64 consecutive
 // rows), no cross-lane work until the workgroup's loss sum.  Each lane adds
 // its rows' loss terms in row order; the workgroup sum is in a fixed order.
@@ -452,13 +459,14 @@ struct FwdPlan {
 FwdPlan plan_forward(int64_t B, int64_t C, bool aligned) {
   FwdPlan p;
   int64_t rows_per_step = 1;
-  if (C <= 32) {
+  if (C <= 32 && !(aligned && C % 4 == 0)) {
     p.lane_cm = C <= 8 ? 8 : C <= 16 ? 16 : 32;
     rows_per_step = kBlock;
   } else if (aligned && C % 4 == 0 && C <= 8192) {
     p.cached = true;
     const int64_t c4 = C / 4;
-    if (c4 <= 64) { p.tpr = 64; p.v = 1; }
+    if (c4 <= 32) { p.tpr = 16; p.v = c4 <= 16 ? 1 : 2; }
+    else if (c4 <= 64) { p.tpr = 64; p.v = 1; }
     else if (c4 <= 256) { p.tpr = 64; p.v = 4; }
     else { p.tpr = 256; p.v = c4 <= 512 ? 2 : c4 <= 1024 ? 4 : 8; }
     const int r = p.v == 1 ? rows_in_flight<1>() : p.v == 2 ? rows_in_flight<2>()
@@ -529,7 +537,9 @@ int softmax_ce_forward_f32(const float* logits, const int64_t* labels, float* lo
       hipLaunchKernelGGL((sce_fwd_kernel<TPR, V, false>), grid, dim3(kBlock), 0, stream,       \
                          logits, labels, lse, slots, key, loss, B, (int)C);                    \
   } while (0)
-    if (p.tpr == 64 && p.v == 1) SCE_FWD(64, 1);
+    if (p.tpr == 16 && p.v == 1) SCE_FWD(16, 1);
+    else if (p.tpr == 16) SCE_FWD(16, 2);
+    else if (p.tpr == 64 && p.v == 1) SCE_FWD(64, 1);
     else if (p.tpr == 64) SCE_FWD(64, 4);
     else if (p.v == 2) SCE_FWD(256, 2);
     else if (p.v == 4) SCE_FWD(256, 4);

@@ -196,6 +196,26 @@ __device__ __forceinline__ float readlane(float v, int lane) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 
+// Sum / max over each 16-lane row of the wave, result in all 16 lanes (the
+// first four steps of the wave reductions below).  Every lane of the row
+// gets the same bits: each step combines the same two partial results, in
+// one order or the other.
+__device__ __forceinline__ float row16_sum_dpp(float v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x141>(v);
+  v += dpp_mov<0x140>(v);
+  return v;
+}
+
+__device__ __forceinline__ float row16_max_dpp(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v));
+  v = fmaxf(v, dpp_mov<0x4E>(v));
+  v = fmaxf(v, dpp_mov<0x141>(v));
+  v = fmaxf(v, dpp_mov<0x140>(v));
+  return v;
+}
+
 __device__ __forceinline__ float wave_sum_dpp(float v) {
   v += dpp_mov<0xB1>(v);
   v += dpp_mov<0x4E>(v);

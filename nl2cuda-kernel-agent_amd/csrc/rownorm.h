@@ -393,16 +393,7 @@ __global__ __launch_bounds__(TPR * H) void rn_bwd_kernel(
 }
 
 // ------------------------------------------- rows of at most 128 floats
-// Sum over each 16-lane row of the wave.  Every lane of the row gets the
-// same bits: each step adds the same two partial sums, in one order or the
-// other.
-__device__ __forceinline__ float row16_sum(float v) {
-  v += dpp_mov<0xB1>(v);
-  v += dpp_mov<0x4E>(v);
-  v += dpp_mov<0x141>(v);
-  v += dpp_mov<0x140>(v);
-  return v;
-}
+__device__ __forceinline__ float row16_sum(float v) { return row16_sum_dpp(v); }
 
 // Rows of at most 128 floats (V = 1 or 2 float4 per lane) take 16 lanes
 // each: four consecutive rows per wave, 16 per block.  Block b walks row

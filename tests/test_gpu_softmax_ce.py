@@ -87,7 +87,8 @@ def test_softmax_ce_bench_shapes(b, c, seed):
                                  (33, 1500), (16, 2048), (9, 3000), (12, 4096), (7, 6000),
                                  (3, 8192), (1, 1), (20, 7), (6, 8196), (4, 12000),
                                  (1000, 32000), (33, 50257), (5, 128256), (4000, 10), (70, 32),
-                                 (300, 17), (64, 33), (1025, 8), (2, 2)])
+                                 (300, 17), (64, 33), (1025, 8), (2, 2), (4097, 64), (999, 128),
+                                 (130, 96), (50, 12)])
 def test_softmax_ce_shapes(b, c):
     announce(f"softmax_ce [{b}, {c}]")
     _check(*_inputs(b, c, b + c))
