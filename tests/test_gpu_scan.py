@@ -108,9 +108,10 @@ def test_scan_i32_to_i64_bit_exact(seed):
     assert torch.equal(y.cpu(), torch.cumsum(x, -1))
 
 
-def test_scan_i32_wrapping_variant():
-    announce("scan int32 -> int32 wrap")
-    x = _ints(8, 70001, 5, -(2**31), 2**31 - 1)
+@pytest.mark.parametrize("rows,d", [(8, 70001), (300, 64), (70, 999)])
+def test_scan_i32_wrapping_variant(rows, d):
+    announce(f"scan int32 -> int32 wrap [{rows}, {d}]")
+    x = _ints(rows, d, 5, -(2**31), 2**31 - 1)
     y = _op().scan_forward_int32(x.cuda())
     torch.cuda.synchronize()
     assert y.dtype == torch.int32
@@ -122,7 +123,9 @@ def test_scan_i32_wrapping_variant():
 
 @pytest.mark.parametrize("rows,d", [(1, 1), (3, 3), (2, 5), (5, 4095), (4, 4096), (3, 4097),
                                     (7, 8191), (2, 65537), (3, 100003), (1, 1 << 20),
-                                    (2, (1 << 21) + 5), (128, 65536), (700, 8192)])
+                                    (2, (1 << 21) + 5), (128, 65536), (700, 8192),
+                                    (65536, 64), (1000, 16), (333, 100), (257, 7), (4097, 256),
+                                    (129, 300), (77, 1000), (1025, 1024), (5, 513), (3, 1025)])
 def test_scan_shapes(rows, d):
     announce(f"scan rows={rows} d={d}")
     op = _op()
