@@ -39,7 +39,7 @@
 //    call wrote.  While the stream is being captured into a graph the call
 //    enqueues a fill kernel over the slots first, so that replays, which
 //    reuse the captured nonce, never read an earlier replay's slots.
-//  * Rows of at most 1024 elements take scan_short_kernel (16 lanes or a
+//  * Rows of at most 2048 elements take scan_short_kernel (16 lanes or a
 //    wave per row, no messages).
 //  * Reverse scans mirror the positions: logical p <-> physical D - 1 - p.
 #include <algorithm>
@@ -62,7 +62,7 @@ constexpr int kTile = kThreads * 4 * kGroups;   // 4096 elements
 constexpr int kWaveSpan = 64 * 4 * kGroups;     // 1024 elements per wave
 constexpr int64_t kMaxChunks = 256;             // chunks per row
 constexpr unsigned kSpinLimit = 1u << 24;       // hang guard for the carry wait
-constexpr int64_t kShortMax = 1024;             // rows up to this take scan_short_kernel
+constexpr int64_t kShortMax = 2048;             // rows up to this take scan_short_kernel
 constexpr int64_t kShortBlocks = 2048;          // its most workgroups
 
 // ------------------------------------------------ 64-bit accumulator helpers
@@ -280,7 +280,7 @@ __device__ __forceinline__ T row16_scan(T v) {
   return v;
 }
 
-// Rows of at most 1024 elements: RL lanes per row (16 up to 256 elements,
+// Rows of at most 2048 elements: RL lanes per row (16 up to 256 elements,
 // 64 above), G 4-element groups per lane at positions 4 (t + RL k), so each
 // load instruction of a row group reads RL x 16 contiguous bytes.  A row
 // group walks every S-th row (S = the grid's row groups); rows need no
@@ -499,7 +499,8 @@ int run(const In* x, Out* y, int64_t rows, int64_t D, void* workspace, size_t ws
     else if (D <= 128) SCAN_SHORT(16, 2);
     else if (D <= 256) SCAN_SHORT(16, 4);
     else if (D <= 512) SCAN_SHORT(64, 2);
-    else SCAN_SHORT(64, 4);
+    else if (D <= 1024) SCAN_SHORT(64, 4);
+    else SCAN_SHORT(64, 8);
 #undef SCAN_SHORT
     return nl2k::check_launch(who);
   }

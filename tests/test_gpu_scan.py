@@ -125,7 +125,8 @@ def test_scan_i32_wrapping_variant(rows, d):
                                     (7, 8191), (2, 65537), (3, 100003), (1, 1 << 20),
                                     (2, (1 << 21) + 5), (128, 65536), (700, 8192),
                                     (65536, 64), (1000, 16), (333, 100), (257, 7), (4097, 256),
-                                    (129, 300), (77, 1000), (1025, 1024), (5, 513), (3, 1025)])
+                                    (129, 300), (77, 1000), (1025, 1024), (5, 513), (3, 1025),
+                                    (33, 2000), (1025, 1537), (7, 2048), (2, 2049)])
 def test_scan_shapes(rows, d):
     announce(f"scan rows={rows} d={d}")
     op = _op()
