@@ -33,7 +33,7 @@ extern "C" {
 #endif
 
 /* Y [N, D] and norm [N] (l2norm_scale.cu:140-150, `l2n_forward`).  The
- * row-cached path runs for D % 4 == 0, D <= 8192 and 16-byte aligned X, g,
+ * row-cached path runs for D % 4 == 0, D <= 16384 and 16-byte aligned X, g,
  * Y; other shapes use generic kernels.  eps >= 0 (NL2K_ERR_VALUE). */
 int l2norm_scale_forward_f32(const float* X, const float* g, float* Y, float* norm, int64_t N,
                              int64_t D, float eps, hipStream_t stream);

@@ -16,9 +16,10 @@
 //   dw = sum over rows of dy xh,  dbias = sum of dy.
 //
 // Design (HBM bound: read x, write y; read dy and x, write dx):
-//  * Row-cached path (D % 4 == 0, 16-byte aligned, D <= 8192): TPR threads
+//  * Row-cached path (D % 4 == 0, 16-byte aligned, D <= 16384): TPR threads
 //    own a row at a time (16 lanes for rows of at most 128 floats, a wave,
-//    or a workgroup of 256 or 512 threads for long rows) and walk every
+//    or a workgroup of 256 or 512 threads for long rows; the backward uses
+//    1024 above 8192 floats) and walk every
 //    S-th row with the next one in flight; each thread keeps V float4 of
 //    the row in registers, so the row is read from HBM exactly once.
 //    Statistics are exact two-pass sums over the registers; reductions are
@@ -64,13 +65,13 @@ __device__ __forceinline__ float dot4(f32x4 a, f32x4 b) {
 }
 __device__ __forceinline__ float hsum4(f32x4 a) { return (a[0] + a[1]) + (a[2] + a[3]); }
 
-// Sum over the TPR threads that share a row (TPR = 64, 256 or 512), result
-// in all of them.  `red` is LDS scratch of at least 2 * TPR / 64 floats per
-// row group; with TPR > 64 every thread of the block must take part (it
-// holds barriers).  The wave totals are added in a fixed order.
+// Sum over the TPR threads that share a row (TPR = 64, 256, 512 or 1024),
+// result in all of them.  `red` is LDS scratch of at least 2 * TPR / 64
+// floats per row group; with TPR > 64 every thread of the block must take
+// part (it holds barriers).  The wave totals are added in a fixed order.
 template <int TPR>
 __device__ __forceinline__ void row_sum2(float& a, float& b, float* red) {
-  static_assert(TPR == 64 || TPR == 256 || TPR == 512, "row width");
+  static_assert(TPR == 64 || TPR == 256 || TPR == 512 || TPR == 1024, "row width");
   a = wave_sum_dpp(a);
   b = wave_sum_dpp(b);
   if constexpr (TPR > 64) {
@@ -84,9 +85,10 @@ __device__ __forceinline__ void row_sum2(float& a, float& b, float* red) {
     __syncthreads();
     a = (red[0] + red[1]) + (red[2] + red[3]);
     b = (red[W] + red[W + 1]) + (red[W + 2] + red[W + 3]);
-    if constexpr (W == 8) {
-      a += (red[4] + red[5]) + (red[6] + red[7]);
-      b += (red[W + 4] + red[W + 5]) + (red[W + 6] + red[W + 7]);
+#pragma unroll
+    for (int q = 4; q < W; q += 4) {
+      a += (red[q] + red[q + 1]) + (red[q + 2] + red[q + 3]);
+      b += (red[W + q] + red[W + q + 1]) + (red[W + q + 2] + red[W + q + 3]);
     }
   }
 }
@@ -109,13 +111,14 @@ __device__ __forceinline__ float row_sum1(float a, float* red) {
 // per row that streamed 47.2 against 44.0 us at [8192, 4096] and 26.6
 // against 25.5 us at [16384, 1024], with identical bits.
 template <class P, int TPR, int V, bool FULL>
-__global__ __launch_bounds__(kBlock) void rn_fwd_kernel(
+__global__ __launch_bounds__(TPR > kBlock ? TPR : kBlock) void rn_fwd_kernel(
     const float* __restrict__ x, const float* __restrict__ w,
     const float* __restrict__ bias, float* __restrict__ y,
     float* __restrict__ stat0, float* __restrict__ stat1, int64_t B,
     int D, float eps) {
-  __shared__ float red[8];
-  constexpr int RPB = kBlock / TPR;
+  constexpr int BS = TPR > kBlock ? TPR : kBlock;  // block size (TPR = 512: one row group)
+  __shared__ float red[TPR >= 256 ? 2 * (TPR / 64) : 1];
+  constexpr int RPB = BS / TPR;
   const int64_t S = (int64_t)gridDim.x * RPB;
   // The row group is wave uniform: from lane 0, so rows and row pointers
   // stay scalar (buffer resources need them so).
@@ -123,7 +126,7 @@ __global__ __launch_bounds__(kBlock) void rn_fwd_kernel(
       (int64_t)blockIdx.x * RPB + __builtin_amdgcn_readfirstlane((int)threadIdx.x) / TPR;
   const int t = threadIdx.x % TPR;
   const int D4 = D >> 2;
-  // TPR = 256: the grid has at most B blocks, so a whole block walks the
+  // TPR >= 256: the grid has at most B blocks, so a whole block walks the
   // same rows and takes the reductions' barriers together.  TPR = 64: a row
   // group past the end leaves (its reductions stay inside its wave).
   if (r0 >= B) return;
@@ -260,7 +263,7 @@ __global__ __launch_bounds__(TPR * H) void rn_bwd_kernel(
     const float* __restrict__ stat1, float* __restrict__ dx,
     float* __restrict__ pw, float* __restrict__ pb, int64_t B, int D) {
   static_assert((TPR == 64 && H == 4) || (TPR == 256 && (H == 1 || H == 2)) ||
-                    (TPR == 512 && H == 1),
+                    ((TPR == 512 || TPR == 1024) && H == 1),
                 "block shape");
   constexpr int kRed = TPR > 64 ? 2 * (TPR / 64) : 1;  // LDS floats per group's row sums
   __shared__ float red[kRed * H];
@@ -281,15 +284,23 @@ __global__ __launch_bounds__(TPR * H) void rn_bwd_kernel(
   const int64_t rlast = r0 < B ? r0 + (B - 1 - r0) / S * S : B - 1;
   const f32x4* w4 = reinterpret_cast<const f32x4*>(w);
 
+  // TPR = 1024 (a block of 16 waves, at most 128 registers a lane) keeps w
+  // in LDS, each thread its own entries, so that the prefetch fits.
+  constexpr bool kWLds = TPR == 1024;
+  __shared__ f32x4 s_w[kWLds ? TPR * V : 1];
   f32x4 wv[V], aw[V], ab[V], gcur[V], xcur[V], gnext[V], xnext[V];
 #pragma unroll
   for (int k = 0; k < V; ++k) {
     const int c = t + k * TPR;
     const f32x4 wk = w4[FULL ? c : min(c, D4 - 1)];
-    wv[k] = (FULL || c < D4) ? wk : zero4();
+    if constexpr (kWLds)
+      s_w[c] = (FULL || c < D4) ? wk : zero4();
+    else
+      wv[k] = (FULL || c < D4) ? wk : zero4();
     aw[k] = zero4();
     ab[k] = zero4();
   }
+  auto w_at = [&](int k) { return kWLds ? s_w[t + k * TPR] : wv[k]; };
   // Ragged rows load through buffer resources (zeros past the row's end,
   // no branch; see the store below).
   auto load_row = [&](int64_t r, f32x4 (&g)[V], f32x4 (&xv)[V]) {
@@ -321,7 +332,7 @@ __global__ __launch_bounds__(TPR * H) void rn_bwd_kernel(
 #pragma unroll
     for (int k2 = 0; k2 < V; ++k2) {
       xh[k2] = (xcur[k2] - mu) * rs;
-      const f32x4 g = gcur[k2] * wv[k2];
+      const f32x4 g = gcur[k2] * w_at(k2);
       if constexpr (P::kCentered) sg += hsum4(g);
       sgx += dot4(g, xh[k2]);
     }
@@ -350,7 +361,7 @@ __global__ __launch_bounds__(TPR * H) void rn_bwd_kernel(
 #pragma unroll
       for (int k2 = 0; k2 < V; ++k2) {
         const int c = t + k2 * TPR;
-        buffer_store4(rdx, rs * (gcur[k2] * wv[k2] - mg - xh[k2] * mgx), (uint32_t)c * 16u, 0);
+        buffer_store4(rdx, rs * (gcur[k2] * w_at(k2) - mg - xh[k2] * mgx), (uint32_t)c * 16u, 0);
       }
     }
 #pragma unroll
@@ -751,7 +762,7 @@ inline int64_t row_groups(int64_t B, int64_t target) {
 
 inline Plan plan(int64_t B, int64_t D, bool aligned) {
   Plan p;
-  p.cached = aligned && D % 4 == 0 && D <= 8192;
+  p.cached = aligned && D % 4 == 0 && D <= 16384;
   if (!p.cached) {
     // ~2048 blocks of 64 columns x (B / S1) rows
     const int64_t slices = ceil_div(D, 64);
@@ -776,9 +787,12 @@ inline Plan plan(int64_t B, int64_t D, bool aligned) {
   } else if (d4 <= 256) {
     p.tpr = 64;
     p.v = (int)ceil_div(d4, 64);  // 2, 3 or 4
-  } else {
+  } else if (d4 <= 2048) {
     p.tpr = 256;
     p.v = d4 <= 512 ? 2 : d4 <= 1024 ? 4 : 8;
+  } else {  // one 512-thread row group per block
+    p.tpr = 512;
+    p.v = 8;
   }
   if (B == 0) return p;
   if (d4 <= 256) {  // a wave per row, four per block
@@ -788,13 +802,14 @@ inline Plan plan(int64_t B, int64_t D, bool aligned) {
     p.G = ceil_div(row_groups(B, p.bv == 1 ? kBwdWaveGroups1 : kBwdWaveGroups2), 4);
   } else {
     // 512-thread blocks (two halves, or 512 threads per row above 4096
-    // floats) fill a CU's two waves per SIMD alone: half as many blocks,
-    // so that all of them are resident at once.
+    // floats) fill a CU's two waves per SIMD alone, as do 1024-thread
+    // blocks (above 8192 floats) its four: half as many blocks, so that all
+    // of them are resident at once.
     if (d4 <= 1024) {
       p.bv = d4 <= 512 ? 2 : 4;
       p.bh = 2;
     } else {
-      p.btpr = 512;
+      p.btpr = d4 <= 2048 ? 512 : 1024;
       p.bv = 4;
     }
     p.G = ceil_div(row_groups(B, kBwdBlocks), 2);
@@ -835,6 +850,16 @@ int run_forward(const float* x, const float* w, const float* bias, float* y, flo
     else
       hipLaunchKernelGGL((rn_fwd_row16_kernel<P, 2>), grid, dim3(kBlock), 0, stream, x, w, bias,
                          y, stat0, stat1, B, (int)D, eps);
+    return check_launch(who);
+  }
+  if (p.cached && p.tpr == 512) {  // one 512-thread row group per block
+    const dim3 grid((unsigned)std::min<int64_t>(B, kFwdBlocks));
+    if (D == 512 * 4 * 8)
+      hipLaunchKernelGGL((rn_fwd_kernel<P, 512, 8, true>), grid, dim3(512), 0, stream, x, w, bias,
+                         y, stat0, stat1, B, (int)D, eps);
+    else
+      hipLaunchKernelGGL((rn_fwd_kernel<P, 512, 8, false>), grid, dim3(512), 0, stream, x, w,
+                         bias, y, stat0, stat1, B, (int)D, eps);
     return check_launch(who);
   }
   if (p.cached) {
@@ -907,7 +932,8 @@ int run_backward(const float* dy, const float* x, const float* w, const float* s
     else if (p.btpr == 64) RN_BWD(64, 4, 4);
     else if (p.bv == 2) RN_BWD(256, 2, 2);
     else if (p.btpr == 256) RN_BWD(256, 4, 2);
-    else RN_BWD(512, 4, 1);
+    else if (p.btpr == 512) RN_BWD(512, 4, 1);
+    else RN_BWD(1024, 4, 1);
 #undef RN_BWD
     st = check_launch(who);
   } else {

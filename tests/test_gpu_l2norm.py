@@ -65,7 +65,8 @@ def test_l2norm_bench_shapes(n, d, seed):
                                  (3, 2048), (513, 1028), (4097, 8192), (1000, 6000),
                                  (4099, 512), (2050, 300),
                                  (16385, 64), (1000, 128), (4097, 96), (4099, 600),
-                                 (1030, 768)])
+                                 (1030, 768), (5, 16384),
+                                 (33, 12288), (3, 20000)])
 def test_l2norm_shapes(n, d):
     announce(f"l2norm_scale [{n}, {d}]")
     _check(*_inputs(n, d, n + d))

@@ -69,7 +69,8 @@ def test_layernorm_baseline_8192x4096(seed):
                                  (1000, 6000), (33, 4100),
                                  (4099, 512), (2050, 300), (16384, 256),
                                  (16385, 64), (1000, 128), (4097, 96), (3, 128), (70, 8),
-                                 (4099, 600), (1030, 768), (257, 1020)])
+                                 (4099, 600), (1030, 768), (257, 1020),
+                                 (5, 16384), (33, 12288), (2, 16380), (700, 10000), (3, 20000)])
 def test_layernorm_shapes(b, d):
     announce(f"layernorm b={b} d={d}")
     _check(*_inputs(b, d, b + d))
