@@ -114,6 +114,15 @@ def test_rbf_generic_feature_dims(d):
     _check_full(*_inputs(70, 45, d, d, scale=1.0 / np.sqrt(d)), 0.5)
 
 
+# the tiled generic kernels: ragged tile edges on both sides, feature chunks
+# of 16 (forward) and passes of 64 (backward) with ragged ends
+@pytest.mark.parametrize("n,m,d", [(130, 200, 16), (257, 65, 128), (1000, 1000, 32),
+                                   (64, 64, 65), (300, 129, 200)])
+def test_rbf_generic_tiled_shapes(n, m, d):
+    announce(f"rbf generic n={n} m={m} D={d}")
+    _check_full(*_inputs(n, m, d, n + m + d, scale=1.0 / np.sqrt(d)), 0.5)
+
+
 def test_rbf_reference_default_distribution():
     announce("rbf gamma=1/64 unscaled inputs (reference defaults)")
     _check_full(*_inputs(512, 384, 64, 11, scale=1.0), 1.0 / 64.0)
@@ -223,6 +232,34 @@ def test_rbf_c_abi_direct():
                                   capi.ptr(dX), capi.ptr(dY), 1024, 768, 64, 0.5,
                                   capi.ptr(ws), ws_bytes - 4, stream)
         assert st != 0 and b"workspace" in lib.rbf_last_error()
+
+
+def test_rbf_generic_backward_split_and_whole():
+    """D != 64: the generic backward cuts its walks into slices when the
+    workspace holds their partial sums, and runs them whole with no
+    workspace; both match the oracle."""
+    announce("rbf generic backward, sliced and whole, 1500 x 700, D=32")
+    lib = _op()._lib()
+    n, m, d = 1500, 700, 32
+    X, Y, G = _inputs(n, m, d, 5, scale=1.0 / np.sqrt(d))
+    Xd, Yd, Gd = X.cuda(), Y.cuda(), G.cuda()
+    K = torch.empty(n, m, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert lib.rbf_forward_f32(capi.ptr(Xd), capi.ptr(Yd), capi.ptr(K), n, m, d, 0.5, stream) == 0
+    ws_bytes = lib.rbf_backward_workspace_bytes(n, m, d)
+    assert ws_bytes > 0
+    ws = torch.empty(ws_bytes // 4, device="cuda")
+    Kr = orbf.forward_f64(X.numpy(), Y.numpy(), 0.5)
+    dXr, dYr = orbf.backward_f64(X.numpy(), Y.numpy(), G.numpy(), Kr, 0.5)
+    for name, ptr, nbytes in (("sliced", capi.ptr(ws), ws_bytes), ("whole", None, 0)):
+        dX = torch.empty_like(Xd)
+        dY = torch.empty_like(Yd)
+        st = lib.rbf_backward_f32(capi.ptr(Xd), capi.ptr(Yd), capi.ptr(Gd), capi.ptr(K),
+                                  capi.ptr(dX), capi.ptr(dY), n, m, d, 0.5, ptr, nbytes, stream)
+        assert st == 0, lib.rbf_last_error()
+        torch.cuda.synchronize()
+        _close(f"dX ({name})", dX, dXr)
+        _close(f"dY ({name})", dY, dYr)
 
 
 def test_rbf_repeatable():
