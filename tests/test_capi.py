@@ -106,8 +106,14 @@ def test_rbf_workspace_plan():
     assert lib.rbf_backward_workspace_bytes(2048, 2048, 64) == 2 * 16 * 2048 * 65 * 4
     assert lib.rbf_backward_workspace_bytes(8192, 8192, 64) == 2 * 32 * 8192 * 65 * 4
     assert lib.rbf_backward_workspace_bytes(64, 64, 64) == 2 * 64 * 65 * 4
-    # other feature widths use the generic path, which needs no workspace
-    assert lib.rbf_backward_workspace_bytes(4096, 4096, 32) == 0
+    # other feature widths use the generic kernels: each side's walk in
+    # slices, 64-aligned, about 1024 workgroups a side.  4096^2, D = 32: 64
+    # row tiles x 1 feature pass -> 16 slices of 256, each a [rows, D]
+    # partial plus a [rows] partial sum, for both sides
+    assert lib.rbf_backward_workspace_bytes(4096, 4096, 32) == 2 * 16 * 4096 * 33 * 4
+    # 100 x 70, D = 200: 2 x 4 tiles, 2 slices of 64 columns for dX; 2 x 4
+    # tiles, 2 slices of 64 rows for dY
+    assert lib.rbf_backward_workspace_bytes(100, 70, 200) == (2 * 100 + 2 * 70) * 201 * 4
 
 
 def test_loader_refuses_without_gpu():
