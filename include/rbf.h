@@ -42,8 +42,11 @@ int rbf_forward_f32(const float* X, const float* Y, float* K, int64_t N,
                     int64_t M, int64_t D, float gamma, hipStream_t stream);
 
 /*
- * Bytes of device workspace rbf_backward_f32 needs for these sizes (the
- * per-region partial sums of dX and dY).  0 means no workspace is needed.
+ * Bytes of device workspace rbf_backward_f32 needs for these sizes: the
+ * per-region partial sums of dX and dY of the tile kernels, or, for shapes
+ * only the generic kernels take (D != 64, N or M past the tile limit), the
+ * partial sums of the slices their walks are cut into.  0 means no
+ * workspace is needed.
  */
 size_t rbf_backward_workspace_bytes(int64_t N, int64_t M, int64_t D);
 
@@ -53,7 +56,9 @@ size_t rbf_backward_workspace_bytes(int64_t N, int64_t M, int64_t D);
  * Tensor K, double gamma) -> [dX, dY]` of the reference
  * (cases/rbf/kernels/rbf_backward.cu:59-88), which cases/rbf/op.py:38 calls.
  * `workspace` must hold rbf_backward_workspace_bytes(N, M, D) bytes (it may
- * be NULL when that is 0).  dX and dY are fully overwritten.
+ * be NULL when that is 0).  A call that takes the generic kernels also runs
+ * with a shorter or NULL workspace, its walks then unsliced (slower, and
+ * rounded differently).  dX and dY are fully overwritten.
  */
 int rbf_backward_f32(const float* X, const float* Y, const float* dK,
                      const float* K, float* dX, float* dY, int64_t N,
@@ -61,8 +66,9 @@ int rbf_backward_f32(const float* X, const float* Y, const float* dK,
                      size_t workspace_bytes, hipStream_t stream);
 
 /*
- * Backward without a caller workspace and without any allocation: the same
- * kernels and results as rbf_backward_f32 (bit for bit), with the region
+ * Backward without a caller workspace and without any allocation: for the
+ * tile kernels the same kernels and results as rbf_backward_f32 (bit for
+ * bit), with the region
  * partials kept in a scratch array compiled into the library (64 MiB per
  * GPU, held from the first call on that GPU until the process ends).  No
  * counterpart in the reference: it is for callers that cannot allocate
@@ -72,8 +78,8 @@ int rbf_backward_f32(const float* X, const float* Y, const float* dK,
  * rbf_backward_workspace_bytes(N, M, D) exceeds
  * rbf_backward_noalloc_max_bytes() are rejected with NL2K_ERR_WORKSPACE
  * before any HIP call (N = M = 4096, D = 64 needs 34 MB and fits; 8192 does
- * not); calls that take the generic kernels use no scratch and run at any
- * size.  Every call on one GPU shares that GPU's scratch, so calls that
+ * not); calls that take the generic kernels use no scratch (their walks
+ * unsliced) and run at any size.  Every call on one GPU shares that GPU's scratch, so calls that
  * overlap in time on one GPU (different streams, or threads) race and must
  * be serialised by the caller; a call needs no initial scratch contents.
  */
