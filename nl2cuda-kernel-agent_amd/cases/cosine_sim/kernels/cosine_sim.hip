@@ -23,13 +23,17 @@
 //    dS . bh and dS^T . ah as region partials (the staged X / Y rows scaled
 //    by inv_a / inv_b); cos_bwd_reduce_kernel sums the partials and applies
 //    the projection, one 16-lane group per row.
-//  * Other feature widths and misaligned pointers use generic kernels.
+//  * Other feature widths and misaligned pointers use the tiled SIMT kernels
+//    of csrc/pairwise_generic.h (rows scaled by their inverse norms as they
+//    are staged), the backward's walks in slices whose partial rows the
+//    projection kernel adds in order.
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
 
 #include "../../../csrc/common.h"
 #include "../../../csrc/pairwise_d64.h"
+#include "../../../csrc/pairwise_generic.h"
 #include "cosine_sim.h"
 
 using nl2k::f32x4;
@@ -136,45 +140,44 @@ __global__ __launch_bounds__(256) void cos_norm_kernel(const float* __restrict__
   }
 }
 
-__global__ __launch_bounds__(256) void cos_fwd_generic_kernel(
-    const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ inv_a,
-    const float* __restrict__ inv_b, float* __restrict__ S, int64_t N, int64_t M, int64_t D) {
-  const int64_t total = N * M;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
-       e += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t i = e / M, j = e - i * M;
-    const float* a = A + i * D;
-    const float* b = B + j * D;
-    const float sa = inv_a[i], sb = inv_b[j];
-    float s = 0.f;
-    for (int64_t d = 0; d < D; ++d) s = fmaf(a[d] * sa, b[d] * sb, s);
-    S[e] = s;
+// Policies of the tiled SIMT kernels (csrc/pairwise_generic.h).
+// Forward: S = sum_d (a_d inv_a) (b_d inv_b), rows scaled as they are staged.
+struct CosGenFwd {
+  const float* __restrict__ inv_a;
+  const float* __restrict__ inv_b;
+  __device__ __forceinline__ float x_in(float v, int64_t i) const { return v * inv_a[i]; }
+  __device__ __forceinline__ float y_in(float v, int64_t j) const { return v * inv_b[j]; }
+  __device__ __forceinline__ float step(float s, float x, float y) const { return fmaf(x, y, s); }
+  __device__ __forceinline__ float out(float s) const { return s; }
+};
+// Backward: dvh[r][d] = sum_o W[r, o] inv_o[o] O[o][d], W = dS (dS^T for the
+// B side); the walked rows are scaled by their inverse norms as staged.
+struct CosGenBwd {
+  const float* __restrict__ inv_a;
+  const float* __restrict__ inv_b;
+  static constexpr bool kSums = false;
+  __device__ __forceinline__ float w(const float* __restrict__ dS, const float*,
+                                     int64_t idx) const {
+    return dS[idx];
   }
-}
-
-// dvh[r][d] = sum_o W[r, o] * inv_o[o] * O[o][d], W = dS (trans: dS^T), one
-// thread per (r, d).
-__global__ __launch_bounds__(256) void cos_bwd_generic_kernel(
-    const float* __restrict__ O, const float* __restrict__ inv_o,
-    const float* __restrict__ dS, float* __restrict__ dvh, int64_t rows, int64_t others,
-    int64_t M, int64_t D, int trans) {
-  const int64_t total = rows * D;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
-       e += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t r = e / D, d = e - r * D;
-    float acc = 0.f;
-    for (int64_t o = 0; o < others; ++o) {
-      const int64_t idx = trans ? o * M + r : r * M + o;
-      acc = fmaf(dS[idx], O[o * D + d] * inv_o[o], acc);
-    }
-    dvh[e] = acc;
+  template <bool TRANS>
+  __device__ __forceinline__ float b_in(float v, int64_t o) const {
+    return v * (TRANS ? inv_a[o] : inv_b[o]);
   }
-}
+  __device__ __forceinline__ float finish(float, float, float acc) const { return acc; }
+};
 
-// out_r = s dvh_r - (vh_r . dvh_r) / |v_r| vh_r, one wave per row.
+// out_r = s dvh_r - (vh_r . dvh_r) / |v_r| vh_r, one wave per row; dvh is
+// the sum, in slice order, of the S partial rows part[s][r][:].
+__device__ __forceinline__ float slice_sum(const float* __restrict__ part, int64_t S,
+                                           int64_t plane, int64_t e) {
+  float v = 0.f;
+  for (int64_t sl = 0; sl < S; ++sl) v += part[sl * plane + e];
+  return v;
+}
 __global__ __launch_bounds__(256) void cos_project_generic_kernel(
-    const float* __restrict__ V, const float* __restrict__ inv, const float* __restrict__ dvh,
-    float* __restrict__ out, int64_t rows, int64_t D) {
+    const float* __restrict__ V, const float* __restrict__ inv, const float* __restrict__ part,
+    int64_t S, float* __restrict__ out, int64_t rows, int64_t D) {
   const int lane = threadIdx.x & 63;
   const int64_t waves = (int64_t)gridDim.x * (blockDim.x / 64);
   for (int64_t r = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6); r < rows;
@@ -183,7 +186,7 @@ __global__ __launch_bounds__(256) void cos_project_generic_kernel(
     float dot = 0.f, nn = 0.f;
     for (int64_t d = lane; d < D; d += 64) {
       const float v = V[r * D + d];
-      dot = fmaf(v * sc, dvh[r * D + d], dot);
+      dot = fmaf(v * sc, slice_sum(part, S, rows * D, r * D + d), dot);
       nn = fmaf(v, v, nn);
     }
     dot = nl2k::wave_sum(dot);
@@ -191,8 +194,16 @@ __global__ __launch_bounds__(256) void cos_project_generic_kernel(
     const float nrm = sqrtf(nn);
     const float coef = nrm > 0.f ? dot / nrm : 0.f;
     for (int64_t d = lane; d < D; d += 64)
-      out[r * D + d] = sc * dvh[r * D + d] - coef * (V[r * D + d] * sc);
+      out[r * D + d] = sc * slice_sum(part, S, rows * D, r * D + d) - coef * (V[r * D + d] * sc);
   }
+}
+
+// Floats of the generic backward's partial rows: S slices a side when
+// `sliced`, one otherwise.
+inline size_t generic_ws_floats(int64_t N, int64_t M, int64_t D, bool sliced) {
+  const int64_t sx = sliced ? nl2k::pairwise::generic_split(N, M, D).s : 1;
+  const int64_t sy = sliced ? nl2k::pairwise::generic_split(M, N, D).s : 1;
+  return (size_t)(sx * N * D + sy * M * D);
 }
 
 __global__ __launch_bounds__(256) void cos_fill_zero_kernel(float* __restrict__ p, size_t count) {
@@ -274,8 +285,11 @@ int cosine_sim_forward_f32(const float* A, const float* B, float* S, float* inv_
   if (st) return st;
   st = launch_norms(B, inv_b, M, D, eps, stream);
   if (st) return st;
-  hipLaunchKernelGGL(cos_fwd_generic_kernel, dim3(grid_for(N * M, 256, 1 << 16)), dim3(256), 0,
-                     stream, A, B, inv_a, inv_b, S, N, M, D);
+  const int64_t ntiles = nl2k::ceil_div(N, (int64_t)nl2k::pairwise::kGT) *
+                         nl2k::ceil_div(M, (int64_t)nl2k::pairwise::kGT);
+  hipLaunchKernelGGL(nl2k::pairwise::pair_fwd_generic_kernel<CosGenFwd>,
+                     dim3((unsigned)std::min<int64_t>(ntiles, 1 << 16)), dim3(256), 0, stream, A,
+                     B, S, N, M, D, CosGenFwd{inv_a, inv_b});
   return nl2k::check_launch("cosine_sim_forward_f32 (generic)");
 }
 
@@ -284,8 +298,10 @@ size_t cosine_sim_backward_workspace_bytes(int64_t N, int64_t M, int64_t D) {
   if (N == 0 || M == 0) return 0;
   const nl2k::pairwise::BwdPlan p = nl2k::pairwise::plan_backward(N, M, D, false);
   const size_t fast = p.fast ? p.ws_floats * sizeof(float) : 0;
-  const size_t generic = (size_t)(N + M) * (size_t)D * sizeof(float);
-  return std::max(fast, generic);
+  // The generic kernels' partial rows: [S][N][D] and [S][M][D] for the
+  // slices of shapes the tile path never takes; one slice a side (the
+  // walks whole) otherwise, which a misaligned call of a tile shape uses.
+  return std::max(fast, generic_ws_floats(N, M, D, !p.fast) * sizeof(float));
 }
 
 int cosine_sim_backward_f32(const float* A, const float* B, const float* inv_a,
@@ -324,22 +340,39 @@ int cosine_sim_backward_f32(const float* A, const float* B, const float* inv_a,
     return nl2k::check_launch("cosine_sim_backward_f32 (reduce)");
   }
 
-  float* dah = ws;                    // [N][D]
-  float* dbh = ws + (size_t)N * D;    // [M][D]
-  hipLaunchKernelGGL(cos_bwd_generic_kernel, dim3(grid_for(N * D, 256, 1 << 16)), dim3(256), 0,
-                     stream, B, inv_b, dS, dah, N, M, M, D, 0);
+  // generic kernels: the walks in slices when the workspace holds their
+  // partial rows, else whole (the entry check above guarantees that much)
+  using nl2k::pairwise::kGT;
+  nl2k::pairwise::GenericSplit gx = nl2k::pairwise::generic_split(N, M, D),
+                               gy = nl2k::pairwise::generic_split(M, N, D);
+  if (workspace_bytes < generic_ws_floats(N, M, D, true) * sizeof(float)) {
+    gx = nl2k::pairwise::generic_whole(M);
+    gy = nl2k::pairwise::generic_whole(N);
+  }
+  float* dah = ws;                               // [Sx][N][D]
+  float* dbh = ws + (size_t)(gx.s * N * D);      // [Sy][M][D]
+  const int64_t dp = nl2k::ceil_div(D, (int64_t)nl2k::pairwise::kGD);
+  const CosGenBwd op{inv_a, inv_b};
+  hipLaunchKernelGGL((nl2k::pairwise::pair_bwd_generic_kernel<CosGenBwd, false>),
+                     dim3((unsigned)std::min<int64_t>(nl2k::ceil_div(N, (int64_t)kGT) * dp * gx.s,
+                                                      1 << 16)),
+                     dim3(256), 0, stream, A, B, dS, nullptr, nullptr, dah, nullptr, N, M, D, gx.s,
+                     gx.chunk, op);
   st = nl2k::check_launch("cosine_sim_backward_f32 (generic dA)");
   if (st) return st;
-  hipLaunchKernelGGL(cos_bwd_generic_kernel, dim3(grid_for(M * D, 256, 1 << 16)), dim3(256), 0,
-                     stream, A, inv_a, dS, dbh, M, N, M, D, 1);
+  hipLaunchKernelGGL((nl2k::pairwise::pair_bwd_generic_kernel<CosGenBwd, true>),
+                     dim3((unsigned)std::min<int64_t>(nl2k::ceil_div(M, (int64_t)kGT) * dp * gy.s,
+                                                      1 << 16)),
+                     dim3(256), 0, stream, B, A, dS, nullptr, nullptr, dbh, nullptr, N, M, D, gy.s,
+                     gy.chunk, op);
   st = nl2k::check_launch("cosine_sim_backward_f32 (generic dB)");
   if (st) return st;
   hipLaunchKernelGGL(cos_project_generic_kernel, dim3(grid_for(N, 4, 1 << 16)), dim3(256), 0,
-                     stream, A, inv_a, dah, dA, N, D);
+                     stream, A, inv_a, dah, gx.s, dA, N, D);
   st = nl2k::check_launch("cosine_sim_backward_f32 (generic project A)");
   if (st) return st;
   hipLaunchKernelGGL(cos_project_generic_kernel, dim3(grid_for(M, 4, 1 << 16)), dim3(256), 0,
-                     stream, B, inv_b, dbh, dB, M, D);
+                     stream, B, inv_b, dbh, gy.s, dB, M, D);
   return nl2k::check_launch("cosine_sim_backward_f32 (generic project B)");
 }
 

@@ -43,6 +43,7 @@
 
 #include "../../../csrc/common.h"
 #include "../../../csrc/pairwise_d64.h"
+#include "../../../csrc/pairwise_generic.h"
 #include "rbf.h"
 
 using nl2k::f32x4;
@@ -125,149 +126,33 @@ __global__ __launch_bounds__(256) void rbf_bwd_reduce_kernel(
 }
 
 // ------------------------------------------------------- generic (any D)
-// Tiled SIMT kernels for the shapes the MFMA engine does not take (D != 64,
-// misaligned pointers, N or M past its limit).  256 threads, a 64 x 64 tile
-// of entries, each thread a 4 x 4 block of them; D is staged through LDS in
-// chunks, k-major, so a thread reads its 4 X and 4 Y values as two float4.
-// Rows or columns past the end, and features past D, load as zeros.
-constexpr int kGT = 64;   // generic tile edge
-constexpr int kGK = 16;   // forward: features per LDS chunk
-constexpr int kGD = 64;   // backward: output features per pass
-
-// K[i][j] = exp(-gamma sum_d (x_id - y_jd)^2), the squared differences
-// summed directly (as the reference kernel does), in feature order.
-__global__ __launch_bounds__(256) void rbf_fwd_generic_kernel(
-    const float* __restrict__ X, const float* __restrict__ Y,
-    float* __restrict__ K, int64_t N, int64_t M, int64_t D, float gamma) {
-  __shared__ float xs[kGK][kGT + 4];
-  __shared__ float ys[kGK][kGT + 4];
-  const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
-  const int64_t ntj = (M + kGT - 1) / kGT, ntiles = (N + kGT - 1) / kGT * ntj;
-  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-  const int64_t i0 = tile / ntj * kGT, j0 = tile % ntj * kGT;
-  float s[4][4] = {};
-  for (int64_t k0 = 0; k0 < D; k0 += kGK) {
-    // 64 rows x 16 features of X and of Y: four of each per thread
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int e = threadIdx.x + 256 * q;  // 0 .. 1023
-      const int r = e / kGK, k = e % kGK;
-      const int64_t gi = i0 + r, gj = j0 + r, gk = k0 + k;
-      const bool kin = gk < D;
-      const float xv = X[min(gi, N - 1) * D + min(gk, D - 1)];
-      const float yv = Y[min(gj, M - 1) * D + min(gk, D - 1)];
-      xs[k][r] = (kin && gi < N) ? xv : 0.f;
-      ys[k][r] = (kin && gj < M) ? yv : 0.f;
-    }
-    __syncthreads();
-#pragma unroll 4
-    for (int k = 0; k < kGK; ++k) {
-      const f32x4 xa = *reinterpret_cast<const f32x4*>(&xs[k][4 * ty]);
-      const f32x4 yb = *reinterpret_cast<const f32x4*>(&ys[k][4 * tx]);
-#pragma unroll
-      for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const float t = xa[a] - yb[b];
-          s[a][b] = fmaf(t, t, s[a][b]);
-        }
-    }
-    __syncthreads();
+// Policies of the tiled SIMT kernels (csrc/pairwise_generic.h).
+struct RbfGenFwd {
+  float gamma;
+  __device__ __forceinline__ float x_in(float v, int64_t) const { return v; }
+  __device__ __forceinline__ float y_in(float v, int64_t) const { return v; }
+  // the squared differences summed directly, as the reference kernel does
+  __device__ __forceinline__ float step(float s, float x, float y) const {
+    const float t = x - y;
+    return fmaf(t, t, s);
   }
-#pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const int64_t i = i0 + 4 * ty + a;
-    if (i >= N) continue;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const int64_t j = j0 + 4 * tx + b;
-      if (j < M) K[i * M + j] = expf(-gamma * s[a][b]);
-    }
+  __device__ __forceinline__ float out(float s) const { return expf(-gamma * s); }
+};
+struct RbfGenBwd {
+  float neg2g;
+  static constexpr bool kSums = true;
+  __device__ __forceinline__ float w(const float* __restrict__ dK, const float* __restrict__ K,
+                                     int64_t idx) const {
+    return dK[idx] * K[idx];
   }
+  template <bool TRANS>
+  __device__ __forceinline__ float b_in(float v, int64_t) const {
+    return v;
   }
-}
-
-// TRANS = false: dX for 64 rows i0.. and 64 features d0..: out[i][d] =
-// neg2g (r_i x_id - sum_j W_ij y_jd), r_i = sum_j W_ij, W = dK o K, j walked
-// in 64-wide tiles in order.  TRANS = true: dY for 64 columns, the same with
-// W transposed (i walked, X in place of Y).  The W tile is read from dK and
-// K once per feature pass, row-contiguous in both cases.  With S > 1 slices
-// the walk is cut into S ranges of `chunk` (a multiple of 64) and each
-// writes its partial sums (pacc [S][rows][D], psum [S][rows]) for
-// rbf_bwd_generic_reduce_kernel; with S == 1 the kernel writes out itself.
-template <bool TRANS>
-__global__ __launch_bounds__(256) void rbf_bwd_generic_kernel(
-    const float* __restrict__ A, const float* __restrict__ Bm,
-    const float* __restrict__ dK, const float* __restrict__ Kf,
-    float* __restrict__ out, float* __restrict__ pacc, float* __restrict__ psum,
-    int64_t N, int64_t M, int64_t D, float neg2g, int64_t S, int64_t chunk) {
-  __shared__ float ws[kGT][kGT + 1];   // W tile, [own][other]
-  __shared__ float bs[kGT][kGD + 4];   // other side's rows, [other][feature]
-  const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
-  const int64_t rows = TRANS ? M : N, others = TRANS ? N : M;
-  const int64_t ndp = (D + kGD - 1) / kGD, ntiles = (rows + kGT - 1) / kGT * ndp * S;
-  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-  const int64_t r0 = tile / (ndp * S) * kGT;
-  const int64_t dpass = tile % (ndp * S) / S, slice = tile % S;
-  const int64_t d0 = dpass * kGD;
-  const int64_t o_end = min(others, (slice + 1) * chunk);
-  float acc[4][4] = {};
-  float rsum[4] = {};
-  for (int64_t o0 = slice * chunk; o0 < o_end; o0 += kGT) {
-    // W tile: 64 x 64 entries, four float per thread, rows of dK / K
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const int e = threadIdx.x + 256 * q;  // 0 .. 4095
-      const int u = e / kGT, v = e % kGT;   // u: row of dK within the tile, v: column
-      const int64_t gi = (TRANS ? o0 : r0) + u, gj = (TRANS ? r0 : o0) + v;
-      const bool in = gi < N && gj < M && (TRANS ? gi : gj) < o_end;
-      const int64_t idx = min(gi, N - 1) * M + min(gj, M - 1);
-      const float wv = dK[idx] * Kf[idx];
-      if (TRANS)
-        ws[v][u] = in ? wv : 0.f;
-      else
-        ws[u][v] = in ? wv : 0.f;
-    }
-    // the other side's 64 rows x 64 features
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const int e = threadIdx.x + 256 * q;
-      const int u = e / kGD, v = e % kGD;
-      const int64_t go = o0 + u, gd = d0 + v;
-      const float bv = Bm[min(go, others - 1) * D + min(gd, D - 1)];
-      bs[u][v] = (go < o_end && gd < D) ? bv : 0.f;
-    }
-    __syncthreads();
-#pragma unroll 4
-    for (int o = 0; o < kGT; ++o) {
-      const f32x4 bb = *reinterpret_cast<const f32x4*>(&bs[o][4 * tx]);
-#pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const float w = ws[4 * ty + a][o];
-        rsum[a] += w;
-#pragma unroll
-        for (int b = 0; b < 4; ++b) acc[a][b] = fmaf(w, bb[b], acc[a][b]);
-      }
-    }
-    __syncthreads();
+  __device__ __forceinline__ float finish(float rs, float a, float acc) const {
+    return neg2g * (rs * a - acc);
   }
-#pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const int64_t r = r0 + 4 * ty + a;
-    if (r >= rows) continue;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const int64_t d = d0 + 4 * tx + b;
-      if (d >= D) continue;
-      if (S == 1)
-        out[r * D + d] = neg2g * (rsum[a] * A[r * D + d] - acc[a][b]);
-      else
-        pacc[(slice * rows + r) * D + d] = acc[a][b];
-    }
-    if (S > 1 && dpass == 0 && tx == 0) psum[slice * rows + r] = rsum[a];
-  }
-  }
-}
+};
 
 // out[r][d] = neg2g (sum_s psum[s][r] a[r][d] - sum_s pacc[s][r][d]), the
 // slices added in order; block b < bx writes dX, the rest dY.
@@ -317,26 +202,11 @@ int validate_sizes(int64_t N, int64_t M, int64_t D) {
   return NL2K_SUCCESS;
 }
 
-// Slices of the generic backward's walk for one side (rows of output,
-// `others` walked): enough that the side has about kGenericBlocks
-// workgroups, each slice a multiple of 64 long.
-constexpr int64_t kGenericBlocks = 1024;
-struct GenericSplit {
-  int64_t s = 1, chunk = 0;
-};
-inline GenericSplit generic_split(int64_t rows, int64_t others, int64_t D) {
-  GenericSplit g;
-  const int64_t tiles = nl2k::ceil_div(rows, (int64_t)kGT) * nl2k::ceil_div(D, (int64_t)kGD);
-  const int64_t otiles = nl2k::ceil_div(others, (int64_t)kGT);
-  const int64_t want = std::min(std::max<int64_t>(1, nl2k::ceil_div(kGenericBlocks, tiles)), otiles);
-  g.chunk = nl2k::ceil_div(otiles, want) * kGT;
-  g.s = nl2k::ceil_div(others, g.chunk);
-  return g;
-}
 // Workspace floats of the generic backward's slices (0 when neither side splits).
 inline size_t generic_ws_floats(int64_t N, int64_t M, int64_t D) {
   if (N <= 0 || M <= 0) return 0;
-  const GenericSplit gx = generic_split(N, M, D), gy = generic_split(M, N, D);
+  const nl2k::pairwise::GenericSplit gx = nl2k::pairwise::generic_split(N, M, D),
+                                     gy = nl2k::pairwise::generic_split(M, N, D);
   if (gx.s == 1 && gy.s == 1) return 0;
   return (size_t)(gx.s * N * (D + 1) + gy.s * M * (D + 1));
 }
@@ -396,14 +266,17 @@ int backward_impl(const float* X, const float* Y, const float* dK, const float* 
 
   // Generic kernels: the walks split into slices when the workspace holds
   // their partial sums (a shorter or no workspace runs them whole).
+  using nl2k::pairwise::kGD;
+  using nl2k::pairwise::kGT;
   const int64_t dp = nl2k::ceil_div(D, (int64_t)kGD);
-  GenericSplit gx = generic_split(N, M, D), gy = generic_split(M, N, D);
+  nl2k::pairwise::GenericSplit gx = nl2k::pairwise::generic_split(N, M, D),
+                               gy = nl2k::pairwise::generic_split(M, N, D);
   const size_t gneed = generic_ws_floats(N, M, D) * sizeof(float);
   float* ws = static_cast<float*>(workspace);
   if (gneed == 0 || ws == nullptr || workspace_bytes < gneed ||
       reinterpret_cast<uintptr_t>(workspace) % 4 != 0) {
-    gx = GenericSplit{1, nl2k::ceil_div(M, (int64_t)kGT) * kGT};
-    gy = GenericSplit{1, nl2k::ceil_div(N, (int64_t)kGT) * kGT};
+    gx = nl2k::pairwise::generic_whole(M);
+    gy = nl2k::pairwise::generic_whole(N);
   }
   float* pxa = ws;
   float* pxs = gx.s > 1 ? pxa + gx.s * N * D : nullptr;
@@ -411,18 +284,18 @@ int backward_impl(const float* X, const float* Y, const float* dK, const float* 
   float* pys = gy.s > 1 ? pya + gy.s * M * D : nullptr;
   if (gx.s == 1) pxa = nullptr;
   if (gy.s == 1) pya = nullptr;
-  hipLaunchKernelGGL(rbf_bwd_generic_kernel<false>,
+  hipLaunchKernelGGL((nl2k::pairwise::pair_bwd_generic_kernel<RbfGenBwd, false>),
                      dim3((unsigned)std::min<int64_t>(
                          nl2k::ceil_div(N, (int64_t)kGT) * dp * gx.s, 1 << 16)),
-                     dim3(256), 0, stream, X, Y, dK, K, dX, pxa, pxs, N, M, D, neg2g, gx.s,
-                     gx.chunk);
+                     dim3(256), 0, stream, X, Y, dK, K, dX, pxa, pxs, N, M, D, gx.s, gx.chunk,
+                     RbfGenBwd{neg2g});
   st = nl2k::check_launch(who);
   if (st) return st;
-  hipLaunchKernelGGL(rbf_bwd_generic_kernel<true>,
+  hipLaunchKernelGGL((nl2k::pairwise::pair_bwd_generic_kernel<RbfGenBwd, true>),
                      dim3((unsigned)std::min<int64_t>(
                          nl2k::ceil_div(M, (int64_t)kGT) * dp * gy.s, 1 << 16)),
-                     dim3(256), 0, stream, Y, X, dK, K, dY, pya, pys, N, M, D, neg2g, gy.s,
-                     gy.chunk);
+                     dim3(256), 0, stream, Y, X, dK, K, dY, pya, pys, N, M, D, gy.s, gy.chunk,
+                     RbfGenBwd{neg2g});
   st = nl2k::check_launch(who);
   if (st || (gx.s == 1 && gy.s == 1)) return st;
   // dX and dY of the split sides in one launch (a side that did not split
@@ -495,9 +368,11 @@ int rbf_forward_f32(const float* X, const float* Y, float* K, int64_t N,
                        nullptr);
     return nl2k::check_launch("rbf_forward_f32");
   }
-  const int64_t ntiles = nl2k::ceil_div(N, (int64_t)kGT) * nl2k::ceil_div(M, (int64_t)kGT);
-  hipLaunchKernelGGL(rbf_fwd_generic_kernel, dim3((unsigned)std::min<int64_t>(ntiles, 1 << 16)),
-                     dim3(256), 0, stream, X, Y, K, N, M, D, gamma);
+  const int64_t ntiles = nl2k::ceil_div(N, (int64_t)nl2k::pairwise::kGT) *
+                         nl2k::ceil_div(M, (int64_t)nl2k::pairwise::kGT);
+  hipLaunchKernelGGL(nl2k::pairwise::pair_fwd_generic_kernel<RbfGenFwd>,
+                     dim3((unsigned)std::min<int64_t>(ntiles, 1 << 16)), dim3(256), 0, stream, X,
+                     Y, K, N, M, D, RbfGenFwd{gamma});
   return nl2k::check_launch("rbf_forward_f32 (generic)");
 }
 

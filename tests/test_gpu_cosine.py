@@ -76,10 +76,21 @@ def test_cosine_square_vs_oracle(n, seed):
 
 
 @pytest.mark.parametrize("n,m,d", [(1000, 3000, 64), (1, 1, 64), (5, 7, 64), (300, 257, 64),
-                                   (129, 65, 32), (200, 150, 100), (64, 64, 1), (3000, 3008, 64)])
+                                   (129, 65, 32), (200, 150, 100), (64, 64, 1), (3000, 3008, 64),
+                                   # tiled generic kernels: ragged tiles, feature chunks and
+                                   # passes, the backward's walks in several slices
+                                   (1000, 1000, 32), (257, 65, 128), (300, 129, 200), (70, 1500, 3)])
 def test_cosine_shapes(n, m, d):
     announce(f"cosine_sim N={n} M={m} D={d}")
     A, B, dS = _inputs(n, m, d, n + m + d)
+    _check(A, B, dS)
+
+
+def test_cosine_generic_zero_rows():
+    announce("cosine_sim generic path, zero rows, D=48")
+    A, B, dS = _inputs(500, 400, 48, 9)
+    A[3] = 0.0
+    B[17] = 0.0
     _check(A, B, dS)
 
 
