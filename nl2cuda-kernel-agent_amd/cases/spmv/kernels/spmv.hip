@@ -44,8 +44,8 @@
 //    lanes of a group share each (col, val) load and read the X row
 //    coalesced, and G groups split a long row's nonzeros (their sums added
 //    by an xor butterfly).  Backward, deterministic and without atomics:
-//    with D % 4 == 0, D <= 64, at most 256 blocks of 256 / L columns
-//    (K <= 4096 at the reference default) and 16-byte aligned X / dY / dX,
+//    with D % 4 == 0, D <= 64, 128 to 256 blocks of 256 / L columns
+//    (K = 4096 at the reference default) and 16-byte aligned X / dY / dX,
 //    two launches: each 1024-position chunk sorts its entries by column
 //    block in LDS, then each column block gathers its segment of every chunk
 //    and sums dY rows per column in registers (the spmm_b_* kernels); else,
@@ -2247,6 +2247,8 @@ struct ColBlockPlan {
   size_t off_rec = 256, off_off = 0, bytes = 0;
 };
 
+constexpr int64_t kColBlockMinKeys = 128;  // column blocks the column-block route needs
+
 ColBlockPlan col_block_plan(int64_t M, int64_t K, int64_t D, int64_t nnz) {
   ColBlockPlan p;
   if (D <= 1 || D > 64 || D % 4 != 0 || M <= 0 || M > INT32_MAX || nnz <= 0 || nnz > INT32_MAX)
@@ -2254,7 +2256,11 @@ ColBlockPlan col_block_plan(int64_t M, int64_t K, int64_t D, int64_t nnz) {
   const int L = D <= 16 ? 4 : 16;
   const int kb = kThreads / L;
   const int64_t n_keys = nl2k::ceil_div(K, (int64_t)kb);
-  if (n_keys > kBktMaxKeys) return p;
+  // Fewer column blocks than this leave most CUs idle in the gather: the
+  // column-major copy is faster there (4096 columns at D = 8, 64 blocks of
+  // 64 columns: 85.7 against 39.8 us; 2048 columns at D = 64, 128 blocks,
+  // stay: 25.7 against 32.9).
+  if (n_keys > kBktMaxKeys || n_keys < kColBlockMinKeys) return p;
   p.use = true;
   p.L = L;
   p.n_keys = (int)n_keys;
