@@ -137,7 +137,9 @@ __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 // 32-bit data format).  A load through it takes a per-lane byte offset in a
 // vector register and a wave-uniform one in a scalar register, so a tile's
 // address costs no vector instructions; a lane offset at or past `bytes`
-// reads zeros.
+// reads zeros.  The bound is checked against the lane offset: a caller that
+// relies on it to drop ragged lanes passes wave_off = 0 (every such caller
+// here does), and a nonzero wave_off is only for accesses known in range.
 typedef __amdgpu_buffer_rsrc_t buffer_rsrc;
 
 __device__ __forceinline__ buffer_rsrc make_rsrc(const void* base, uint32_t bytes) {
